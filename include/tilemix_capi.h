@@ -1,0 +1,150 @@
+#ifndef TILEMIX_CAPI_H
+#define TILEMIX_CAPI_H
+/*
+ * C ABI of the MI355X TileMix library (libtilemix_hip.so).
+ *
+ * Plain pointers, sizes and ints only, so that ctypes / cgo / JNI / N-API can
+ * bind it without C++ or HIP headers:
+ *   - fp16 tensors are passed as `uint16_t*` holding IEEE binary16 bit
+ *     patterns (the storage of `__half`);
+ *   - every pointer is a device pointer owned by the caller; the library
+ *     allocates nothing and keeps no state between calls;
+ *   - `stream` is a `hipStream_t` (NULL = the default stream); all work is
+ *     enqueued on it and nothing synchronises;
+ *   - the return value is a `hipError_t` code (0 = hipSuccess). Argument
+ *     errors are reported before any HIP runtime call, so they can be tested
+ *     on a machine without a GPU.
+ *
+ * include/attention_fused.h wraps these in the reference's C++ signatures.
+ */
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error codes returned (numeric values of hipError_t). */
+#define TILEMIX_SUCCESS 0                     /* hipSuccess */
+#define TILEMIX_ERROR_INVALID_VALUE 1         /* hipErrorInvalidValue */
+#define TILEMIX_ERROR_INVALID_CONFIGURATION 9 /* hipErrorInvalidConfiguration */
+#define TILEMIX_ERROR_NOT_SUPPORTED 801       /* hipErrorNotSupported */
+
+/*
+ * Replaces quantize_tilemix_qk (reference include/attention_fused.h:62-65,
+ * src/tilemix.cu:223-236).
+ * Symmetric INT8 quantization of Q in 128-row blocks and K in 64-row blocks:
+ * scale = fp32(absmax / 127) (IEEE round-to-nearest), stored as fp16;
+ * value = clamp(trunc(x/scale + copysign(0.5, x/scale)), -127, 127), 0 when
+ * the block is all zeros. Q8[M*d], K8[N*d], q_scales[ceil(M/128)],
+ * k_scales[ceil(N/64)]. Errors: null pointer or M, N, d <= 0 ->
+ * InvalidValue; d > 128 -> NotSupported.
+ */
+int tilemix_quantize_qk(const uint16_t* Q, const uint16_t* K, int8_t* Q8, int8_t* K8,
+                        uint16_t* q_scales, uint16_t* k_scales, int M, int N, int d,
+                        void* stream);
+
+/*
+ * Replaces launch_fused_fp16_attention (reference include/attention_fused.h:68-72,
+ * src/tilemix.cu:238-278); TileMixRouting and TileMixQuantized
+ * (attention_fused.h:47-60) are flattened into their fields.
+ * O[M*d] (fp32) = softmax(score_scale * route(Q K^T)) V for one head, where
+ * the route of each 16-row x 32-key cell is bit (ktile / key_tiles_per_group)
+ * of routing word [qtile * words_per_row + group / 64]: 1 = INT8 scores
+ * (exact int32 dot of Q8/K8 rows times q_scales[q/128] * k_scales[k/64]),
+ * 0 = FP16 scores (fp16 products, fp32 accumulation). route_words == NULL
+ * means every cell is FP16. decoded_bits (optional, ceil(M/16)*ceil(N/32)
+ * bytes) receives the decoded bit of every cell; score_dots (optional, M*N
+ * int32) receives the raw int32 dot of every INT8-routed (q, k).
+ * Validation order and codes follow src/tilemix.cu:242-266.
+ */
+int tilemix_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* O,
+                      int M, int N, int d, float score_scale, void* stream,
+                      const uint64_t* route_words, size_t route_word_count,
+                      int key_tiles_per_group, uint8_t* decoded_bits,
+                      const int8_t* Q8, const int8_t* K8, const uint16_t* q_scales,
+                      const uint16_t* k_scales, int32_t* score_dots);
+
+/* Routing codes written to decoded_bits by the batched entry point. */
+#define TILEMIX_ROUTE_FP16 0
+#define TILEMIX_ROUTE_INT8 1
+#define TILEMIX_ROUTE_SKIP 2
+
+/*
+ * Batched multi-head problem for tilemix_attention_batched /
+ * tilemix_quantize_qk_batched. No reference counterpart: the reference API is
+ * one head per call; this runs `heads` independent heads in one launch, each
+ * laid out exactly as the per-head API expects (rows of d contiguous
+ * elements), head h starting at base + h * <x>_head_stride elements.
+ *
+ * Extensions over the per-head API:
+ *   causal      key k is visible to query q only when k <= q;
+ *   skip_words  same packing and size as route_words; a set bit removes the
+ *               whole cell (its scores are -inf). A query row left with no
+ *               visible key gets O = 0;
+ *   precise     0: P is rounded to fp16 for the P.V MFMA (fast);
+ *               1: P is split into fp16 hi + lo parts (two MFMAs), giving
+ *                  fp32-level accuracy;
+ *   quantize    1: the call quantizes Q and K itself: the K blocks are
+ *               quantized by a pre-pass into K8 / k_scales (required outputs),
+ *               each workgroup quantizes its own 128-row Q block in registers,
+ *               and Q8 / q_scales, if non-NULL, receive the Q result;
+ *               0: Q8/K8/q_scales/k_scales are caller-provided inputs (as
+ *               produced by tilemix_quantize_qk_batched).
+ * Per-head sizes: route/skip words tilemix_routing_word_count(M, N, g);
+ * decoded_bits ceil(M/16)*ceil(N/32) bytes; score_dots M*N; Q8 M*d; K8 N*d;
+ * q_scales ceil(M/128); k_scales ceil(N/64) - all contiguous per head.
+ */
+typedef struct TileMixBatchedArgs {
+    const uint16_t* Q;
+    const uint16_t* K;
+    const uint16_t* V;
+    float* O;
+    int heads;
+    int M;
+    int N;
+    int d;
+    int64_t q_head_stride;
+    int64_t k_head_stride;
+    int64_t v_head_stride;
+    int64_t o_head_stride;
+    float score_scale;
+    int causal;
+    int precise;
+    int quantize;
+    const uint64_t* route_words;
+    const uint64_t* skip_words;
+    int key_tiles_per_group;
+    uint8_t* decoded_bits;
+    int8_t* Q8;
+    int8_t* K8;
+    uint16_t* q_scales;
+    uint16_t* k_scales;
+    int32_t* score_dots;
+} TileMixBatchedArgs;
+
+/* Multi-head attention (extension, see TileMixBatchedArgs). */
+int tilemix_attention_batched(const TileMixBatchedArgs* args, void* stream);
+
+/* Multi-head quantizer (extension): tilemix_quantize_qk for each of `heads`
+ * heads, head h of Q/K at h * {q,k}_head_stride elements, outputs contiguous
+ * per head (Q8 M*d, K8 N*d, q_scales ceil(M/128), k_scales ceil(N/64)). Either
+ * side may be skipped by passing NULL for both its input and outputs. */
+int tilemix_quantize_qk_batched(const uint16_t* Q, const uint16_t* K, int8_t* Q8, int8_t* K8,
+                                uint16_t* q_scales, uint16_t* k_scales, int heads, int M,
+                                int N, int d, int64_t q_head_stride, int64_t k_head_stride,
+                                void* stream);
+
+/* FFI mirrors of the constexpr sizing helpers of attention_fused.h:21-45, for
+ * callers that cannot evaluate C++ constexpr functions. */
+size_t tilemix_routing_words_per_row_c(int N, int key_tiles_per_group);
+size_t tilemix_routing_word_count_c(int M, int N, int key_tiles_per_group);
+size_t tilemix_shared_bytes_c(int d, int quantized);
+
+/* Library version string, e.g. "tilemix-hip 0.1 gfx950". */
+const char* tilemix_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TILEMIX_CAPI_H */

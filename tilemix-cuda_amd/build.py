@@ -1,0 +1,129 @@
+"""Build the gfx950 TileMix library and its native drivers with hipcc.
+
+Outputs (in-tree, git-ignored, shipped with the tree to the GPU host):
+  tilemix-cuda_amd/libtilemix_hip.so        the library (C ABI of include/tilemix_capi.h)
+  tilemix-cuda_amd/_build/tilemix_demo      demo driver (restates the reference src/main.cu)
+  tests/native/_build/tilemix_test          native test driver (restates src/tests/tilemix_test.cu)
+
+Usage: python tilemix-cuda_amd/build.py [--lib-only] [--jobs N]
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+ROOT = PACKAGE.parent
+CSRC = PACKAGE / "csrc"
+INCLUDE = ROOT / "include"
+BUILD = PACKAGE / "_build"
+LIBRARY = PACKAGE / "libtilemix_hip.so"
+NATIVE_TEST_DIR = ROOT / "tests" / "native"
+NATIVE_TEST = NATIVE_TEST_DIR / "_build" / "tilemix_test"
+DEMO = BUILD / "tilemix_demo"
+ORACLE_DIR = ROOT / "oracle"
+
+HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+# Device flags: IEEE binary32 division for the bit-exact quantizer, and no
+# packed-FP32 VALU instructions (v_pk_*_f32) in generated code.
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-mcode-object-version=5",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-fno-fast-math",
+    "-ffp-contract=fast",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+]
+
+LIB_SOURCES = ["quantize.hip", "attention.hip"]
+
+
+def _run(cmd: list[str]) -> None:
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature flag; that
+    # warning is expected and filtered.
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in result.stderr.splitlines() if noise not in line)
+    if result.returncode != 0:
+        raise RuntimeError(f"command failed ({result.returncode}): {' '.join(cmd)}\n{err}\n{result.stdout}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def compile_object(source: Path, obj: Path) -> Path:
+    obj.parent.mkdir(parents=True, exist_ok=True)
+    _run([HIPCC, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(source), "-o", str(obj)])
+    return obj
+
+
+def build_library(jobs: int) -> Path:
+    BUILD.mkdir(parents=True, exist_ok=True)
+    with futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objects = list(pool.map(lambda s: compile_object(CSRC / s, BUILD / (s + ".o")), LIB_SOURCES))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)])
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+def build_oracle() -> None:
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+
+
+def build_native_test() -> Path:
+    """tests/native/tilemix_test.cpp links the library and (as its checker) the oracle."""
+    NATIVE_TEST.parent.mkdir(parents=True, exist_ok=True)
+    oracle_obj = NATIVE_TEST.parent / "tilemix_oracle.o"
+    _run(["gcc", "-O2", "-std=c99", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
+          "-c", str(ORACLE_DIR / "tilemix_oracle.c"), "-o", str(oracle_obj)])
+    tmp = NATIVE_TEST.with_suffix(".tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", f"-I{INCLUDE}", f"-I{ORACLE_DIR}",
+          str(NATIVE_TEST_DIR / "tilemix_test.cpp"), str(oracle_obj), "-fopenmp",
+          f"-L{PACKAGE}", "-ltilemix_hip", f"-Wl,-rpath,{PACKAGE}", "-Wl,-rpath,$ORIGIN/../../../tilemix-cuda_amd",
+          "-o", str(tmp)])
+    os.replace(tmp, NATIVE_TEST)
+    return NATIVE_TEST
+
+
+def build_demo() -> Path:
+    tmp = DEMO.with_suffix(".tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", f"-I{INCLUDE}",
+          str(PACKAGE / "examples" / "demo_main.cpp"), f"-L{PACKAGE}", "-ltilemix_hip",
+          f"-Wl,-rpath,{PACKAGE}", "-Wl,-rpath,$ORIGIN/..", "-o", str(tmp)])
+    os.replace(tmp, DEMO)
+    return DEMO
+
+
+def build_all(lib_only: bool = False, jobs: int | None = None) -> None:
+    jobs = jobs or min(8, os.cpu_count() or 1)
+    build_library(jobs)
+    if lib_only:
+        return
+    build_oracle()
+    build_native_test()
+    build_demo()
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--lib-only", action="store_true")
+    parser.add_argument("--jobs", type=int, default=None)
+    args = parser.parse_args()
+    build_all(lib_only=args.lib_only, jobs=args.jobs)
+    print(f"built {LIBRARY}")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,155 @@
+// Block INT8 quantizer for TileMix on gfx950.
+//
+// Replaces quantize_tilemix_qk / quantize_blocks<BlockRows> of the reference
+// (src/tilemix.cu:16-49, 223-236). One 256-thread workgroup owns one
+// quantization block (128 Q rows or 64 K rows x d features). Because rows are
+// contiguous, a block is one contiguous span of rows*d halves: the vector path
+// reads it once with 16-byte loads into registers (at most 8 per thread),
+// reduces the absmax across the workgroup and quantizes from registers, so HBM
+// sees exactly one read of the input and one write of the int8 output.
+
+#include "tilemix_device.h"
+#include "tilemix_launch.h"
+
+namespace tilemix {
+namespace {
+
+constexpr int kQuantThreads = 256;
+constexpr int kQuantMaxChunks = (128 * 128 / 8) / kQuantThreads;  // 16-byte chunks per thread
+
+template <bool kVector>
+__global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSide q, QuantSide k, int d) {
+    __shared__ float partial[kQuantThreads / kWave];
+    const bool is_q = static_cast<int>(blockIdx.x) < q.blocks;
+    const QuantSide side = is_q ? q : k;
+    const int block = is_q ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x) - q.blocks;
+    const std::int64_t head = blockIdx.y;
+    const int first = block * side.block_rows;
+    const int last = min(side.rows, first + side.block_rows);
+    const int count = (last - first) * d;
+    const std::uint16_t* in = side.x + head * side.in_head_stride + static_cast<std::int64_t>(first) * d;
+    std::int8_t* out = side.x8 + head * static_cast<std::int64_t>(side.rows) * d +
+                       static_cast<std::int64_t>(first) * d;
+    const int t = threadIdx.x;
+
+    float absmax = 0.0f;
+    uint4v chunk[kQuantMaxChunks];
+    const int chunks = count / 8;
+    if constexpr (kVector) {
+#pragma unroll
+        for (int c = 0; c < kQuantMaxChunks; ++c) {
+            const int index = t + c * kQuantThreads;
+            if (index < chunks) {
+                chunk[c] = reinterpret_cast<const uint4v*>(in)[index];
+                const half8 h = __builtin_bit_cast(half8, chunk[c]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) absmax = fmaxf(absmax, fabsf(static_cast<float>(h[e])));
+            }
+        }
+    } else {
+        for (int index = t; index < count; index += kQuantThreads)
+            absmax = fmaxf(absmax, fabsf(half_bits_to_float(in[index])));
+    }
+
+    absmax = wave_max(absmax);
+    if ((t & (kWave - 1)) == 0) partial[t / kWave] = absmax;
+    __syncthreads();
+    absmax = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
+    const float scale = block_scale(absmax);
+    if (t == 0) side.scales[head * side.blocks + block] = float_to_half_bits(scale);
+
+    if constexpr (kVector) {
+#pragma unroll
+        for (int c = 0; c < kQuantMaxChunks; ++c) {
+            const int index = t + c * kQuantThreads;
+            if (index < chunks) {
+                const half8 h = __builtin_bit_cast(half8, chunk[c]);
+                int v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = quantize_value(static_cast<float>(h[e]), scale);
+                uint2v packed;
+                packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
+                packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);
+                reinterpret_cast<uint2v*>(out)[index] = packed;
+            }
+        }
+    } else {
+        for (int index = t; index < count; index += kQuantThreads)
+            out[index] = static_cast<std::int8_t>(quantize_value(half_bits_to_float(in[index]), scale));
+    }
+}
+
+bool aligned(const void* pointer, std::size_t bytes) {
+    return (reinterpret_cast<std::uintptr_t>(pointer) % bytes) == 0;
+}
+
+}  // namespace
+
+hipError_t launch_quantize(const QuantSide& q, const QuantSide& k, int heads, int d,
+                           hipStream_t stream) {
+    const int blocks = q.blocks + k.blocks;
+    if (blocks == 0) return hipSuccess;
+    if (heads > 65535) return hipErrorInvalidConfiguration;
+    // The vector path reads 16-byte chunks of halves and writes 8-byte chunks
+    // of int8; rows of d % 8 == 0 halves keep every block start aligned.
+    bool vector = d % 8 == 0;
+    for (const QuantSide* side : {&q, &k}) {
+        if (side->blocks == 0) continue;
+        vector = vector && aligned(side->x, 16) && aligned(side->x8, 8) &&
+                 (side->in_head_stride * 2) % 16 == 0;
+    }
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(heads));
+    if (vector)
+        quantize_blocks_kernel<true><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
+    else
+        quantize_blocks_kernel<false><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
+    return hipGetLastError();
+}
+
+QuantSide make_quant_side(const std::uint16_t* x, std::int8_t* x8, std::uint16_t* scales,
+                          std::int64_t head_stride, int rows, int block_rows) {
+    QuantSide side{};
+    side.x = x;
+    side.x8 = x8;
+    side.scales = scales;
+    side.in_head_stride = head_stride;
+    side.rows = rows;
+    side.block_rows = block_rows;
+    side.blocks = x ? (rows - 1) / block_rows + 1 : 0;
+    return side;
+}
+
+}  // namespace tilemix
+
+extern "C" int tilemix_quantize_qk(const std::uint16_t* Q, const std::uint16_t* K, std::int8_t* Q8,
+                                   std::int8_t* K8, std::uint16_t* q_scales, std::uint16_t* k_scales,
+                                   int M, int N, int d, void* stream) {
+    // Validation order of src/tilemix.cu:227-230.
+    if (!Q || !K || !Q8 || !K8 || !q_scales || !k_scales || M <= 0 || N <= 0 || d <= 0)
+        return hipErrorInvalidValue;
+    if (d > tilemix::kMaxHeadDim) return hipErrorNotSupported;
+    const auto q = tilemix::make_quant_side(Q, Q8, q_scales, 0, M, tilemix::kQBlockRows);
+    const auto k = tilemix::make_quant_side(K, K8, k_scales, 0, N, tilemix::kKBlockRows);
+    return tilemix::launch_quantize(q, k, 1, d, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tilemix_quantize_qk_batched(const std::uint16_t* Q, const std::uint16_t* K,
+                                           std::int8_t* Q8, std::int8_t* K8,
+                                           std::uint16_t* q_scales, std::uint16_t* k_scales,
+                                           int heads, int M, int N, int d,
+                                           std::int64_t q_head_stride, std::int64_t k_head_stride,
+                                           void* stream) {
+    const bool q_side = Q || Q8 || q_scales;
+    const bool k_side = K || K8 || k_scales;
+    if ((q_side && (!Q || !Q8 || !q_scales)) || (k_side && (!K || !K8 || !k_scales)) ||
+        (!q_side && !k_side) || heads <= 0 || d <= 0 || (q_side && M <= 0) ||
+        (k_side && N <= 0) || (q_side && heads > 1 && q_head_stride < static_cast<std::int64_t>(M) * d) ||
+        (k_side && heads > 1 && k_head_stride < static_cast<std::int64_t>(N) * d))
+        return hipErrorInvalidValue;
+    if (d > tilemix::kMaxHeadDim) return hipErrorNotSupported;
+    const auto q = tilemix::make_quant_side(q_side ? Q : nullptr, Q8, q_scales, q_head_stride,
+                                            q_side ? M : 1, tilemix::kQBlockRows);
+    const auto k = tilemix::make_quant_side(k_side ? K : nullptr, K8, k_scales, k_head_stride,
+                                            k_side ? N : 1, tilemix::kKBlockRows);
+    return tilemix::launch_quantize(q, k, heads, d, static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,64 @@
+#pragma once
+// Device-side building blocks shared by the gfx950 TileMix kernels.
+//
+// Build requirements (set by tilemix-cuda_amd/build.py): --offload-arch=gfx950,
+// -fhip-fp32-correctly-rounded-divide-sqrt (binary32 '/' is IEEE
+// round-to-nearest, which the quantizer's bit-exact contract depends on) and no
+// fast-math flags.
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace tilemix {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef unsigned int uint4v __attribute__((ext_vector_type(4)));
+typedef unsigned int uint2v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+
+inline constexpr int kWave = 64;
+
+__device__ __forceinline__ float half_bits_to_float(std::uint16_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+}
+
+// binary32 -> binary16, round to nearest even (v_cvt_f16_f32 in the default
+// rounding mode), matching __float2half_rn.
+__device__ __forceinline__ std::uint16_t float_to_half_bits(float value) {
+    return __builtin_bit_cast(std::uint16_t, static_cast<_Float16>(value));
+}
+
+// Symmetric INT8 quantization of one element (reference src/tilemix.cu:44-46):
+// the IEEE quotient by the fp32 block scale, a binary32 add of +-0.5, then
+// truncation toward zero and a clamp to [-127, 127]. Keeping the rounded add
+// (rather than an exact round-half-away) is part of the bit-exact contract.
+__device__ __forceinline__ int quantize_value(float x, float scale) {
+    const float normalized = scale > 0.0f ? x / scale : 0.0f;
+    const float shifted = normalized + __builtin_copysignf(0.5f, normalized);
+    const int rounded = static_cast<int>(shifted);
+    return rounded < -127 ? -127 : (rounded > 127 ? 127 : rounded);
+}
+
+// Block scale: fp32 absmax / 127 with IEEE rounding (src/tilemix.cu:37).
+__device__ __forceinline__ float block_scale(float absmax) { return absmax / 127.0f; }
+
+__device__ __forceinline__ float wave_max(float value) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset));
+    return value;
+}
+
+// Packs four quantized values (low byte first) into one 32-bit word.
+__device__ __forceinline__ std::uint32_t pack_bytes(int a, int b, int c, int d) {
+    return (static_cast<std::uint32_t>(a) & 0xffu) | ((static_cast<std::uint32_t>(b) & 0xffu) << 8) |
+           ((static_cast<std::uint32_t>(c) & 0xffu) << 16) | (static_cast<std::uint32_t>(d) << 24);
+}
+
+}  // namespace tilemix
