@@ -89,8 +89,12 @@ int tilemix_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* V, f
  *               quantized by a pre-pass into K8 / k_scales (required outputs),
  *               each workgroup quantizes its own 128-row Q block in registers,
  *               and Q8 / q_scales, if non-NULL, receive the Q result;
+ *               2: as 1, but K8 / k_scales are caller-provided inputs (e.g.
+ *               a key cache quantized once by tilemix_quantize_qk_batched);
  *               0: Q8/K8/q_scales/k_scales are caller-provided inputs (as
  *               produced by tilemix_quantize_qk_batched).
+ *               Only INT8-routed cells read the quantized operands, so they
+ *               are required only when route_words is non-NULL.
  * Per-head sizes: route/skip words tilemix_routing_word_count(M, N, g);
  * decoded_bits ceil(M/16)*ceil(N/32) bytes; score_dots M*N; Q8 M*d; K8 N*d;
  * q_scales ceil(M/128); k_scales ceil(N/64) - all contiguous per head.

@@ -88,20 +88,24 @@ def build_native_test() -> Path:
     oracle_obj = NATIVE_TEST.parent / "tilemix_oracle.o"
     _run(["gcc", "-O2", "-std=c99", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
           "-c", str(ORACLE_DIR / "tilemix_oracle.c"), "-o", str(oracle_obj)])
-    tmp = NATIVE_TEST.with_suffix(".tmp")
+    test_obj = NATIVE_TEST.parent / "tilemix_test.o"
     _run([HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", f"-I{INCLUDE}", f"-I{ORACLE_DIR}",
-          str(NATIVE_TEST_DIR / "tilemix_test.cpp"), str(oracle_obj), "-fopenmp",
-          f"-L{PACKAGE}", "-ltilemix_hip", f"-Wl,-rpath,{PACKAGE}", "-Wl,-rpath,$ORIGIN/../../../tilemix-cuda_amd",
-          "-o", str(tmp)])
+          "-Wno-unused-command-line-argument", "-c", str(NATIVE_TEST_DIR / "tilemix_test.cpp"),
+          "-o", str(test_obj)])
+    tmp = NATIVE_TEST.with_suffix(".tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", str(test_obj), str(oracle_obj), "-fopenmp",
+          f"-L{PACKAGE}", "-ltilemix_hip", "-Wl,-rpath,$ORIGIN/../../../tilemix-cuda_amd", "-o", str(tmp)])
     os.replace(tmp, NATIVE_TEST)
     return NATIVE_TEST
 
 
 def build_demo() -> Path:
-    tmp = DEMO.with_suffix(".tmp")
+    obj = BUILD / "demo_main.o"
     _run([HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", f"-I{INCLUDE}",
-          str(PACKAGE / "examples" / "demo_main.cpp"), f"-L{PACKAGE}", "-ltilemix_hip",
-          f"-Wl,-rpath,{PACKAGE}", "-Wl,-rpath,$ORIGIN/..", "-o", str(tmp)])
+          "-Wno-unused-command-line-argument", "-c", str(PACKAGE / "examples" / "demo_main.cpp"), "-o", str(obj)])
+    tmp = DEMO.with_suffix(".tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", str(obj), f"-L{PACKAGE}", "-ltilemix_hip",
+          "-Wl,-rpath,$ORIGIN/..", "-o", str(tmp)])
     os.replace(tmp, DEMO)
     return DEMO
 

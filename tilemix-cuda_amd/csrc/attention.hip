@@ -671,6 +671,7 @@ extern "C" int tilemix_attention_batched(const TileMixBatchedArgs* args, void* s
             return hipErrorInvalidValue;
     }
     const bool int8 = a.route_words != nullptr;
+    if (a.quantize < 0 || a.quantize > 2) return hipErrorInvalidValue;
     if (int8) {
         if (!a.K8 || !a.k_scales) return hipErrorInvalidValue;
         if (!a.quantize && (!a.Q8 || !a.q_scales)) return hipErrorInvalidValue;
@@ -678,7 +679,7 @@ extern "C" int tilemix_attention_batched(const TileMixBatchedArgs* args, void* s
     } else if (a.score_dots) {
         return hipErrorInvalidValue;
     }
-    if (a.quantize && int8) {
+    if (a.quantize == 1 && int8) {
         const QuantSide none = make_quant_side(nullptr, nullptr, nullptr, 0, 1, kQBlockRows);
         const QuantSide k = make_quant_side(a.K, a.K8, a.k_scales, a.k_head_stride, a.N, kKBlockRows);
         const hipError_t status = check_device();

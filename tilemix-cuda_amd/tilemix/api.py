@@ -172,7 +172,7 @@ class BatchedArgs:
     o_head_stride: int = 0
     causal: bool = False
     precise: bool = False
-    quantize: bool = True
+    quantize: int = 1  # 0: Q8/K8 given, 1: quantize Q and K, 2: K8 given, quantize Q
     route_words: Any = None
     skip_words: Any = None
     key_tiles_per_group: int = 1
