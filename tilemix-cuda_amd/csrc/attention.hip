@@ -17,9 +17,16 @@
 //    v_mfma_f32_16x16x32_f16; the V^T operand is read from the row-major V
 //    tile in LDS with ds_read_b64_tr_b16, which transposes 16-bit elements
 //    across each 16-lane group. Key order inside a 32-key MFMA step is
-//    permuted identically on both operands.
+//    permuted identically on both operands. Row sums come from the same
+//    MFMA with an all-ones operand.
+//  * K, K8 and V tiles move HBM -> LDS with buffer_load ... lds (no VGPR
+//    staging): per-lane offsets into the padded, bank-conflict-free LDS rows
+//    are computed once, each tile only changes a scalar offset, and rows past
+//    the end of the head read as zero. The V tile is fetched while the
+//    scores are computed and the next K tile while softmax and P.V run, with
+//    two barriers per tile and 44 KiB of LDS so two workgroups share a CU.
 //  * A 16x32 routing cell covers whole 16x16 MFMA blocks, so each route is
-//    uniform per MFMA and the branch is taken on scalar route bits.
+//    uniform per MFMA and the branch is taken on wave-uniform route masks.
 //  * The optional in-kernel Q quantization reproduces quantize_tilemix_qk's
 //    bytes exactly: the workgroup's 128 rows are exactly one Q block.
 
@@ -35,10 +42,19 @@ namespace tilemix {
 namespace {
 
 constexpr int kThreadsPerGroup = 256;
+constexpr int kWavesPerGroup = kThreadsPerGroup / kWave;
 constexpr int kRowsPerGroup = 128;  // one Q quantization block
 constexpr int kRowsPerWave = 32;
 constexpr int kTileKeys = 64;  // one K quantization block
+#ifndef TILEMIX_GROUPS_PER_CU
+#define TILEMIX_GROUPS_PER_CU 2
+#endif
+// Workgroups per CU the register allocation is sized for (launch bound).
+constexpr int kGroupsPerCU = TILEMIX_GROUPS_PER_CU;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kXcds = 8;                        // MI355X: 8 XCDs, workgroups dealt round-robin
+constexpr std::uint32_t kBufferFlags = 0x00020000u;  // raw buffer resource word 3, gfx9 family
+constexpr int kOutOfRange = static_cast<int>(0x80000000u);  // buffer offset that reads as zero
 
 struct AttnParams {
     const std::uint16_t* Q;
@@ -77,33 +93,32 @@ struct AttnParams {
     float score_scale;
 };
 
-// Route code of one 16x32 cell: 0 = FP16, 1 = INT8, 2 = skip. Cells outside
-// the problem report skip so that no work is done for them.
-__device__ __forceinline__ int cell_code(const AttnParams& p, std::int64_t head, int qt, int kt) {
-    if (qt >= p.q_tiles16 || kt >= p.key_tiles32) return 2;
-    const std::int64_t group = kt / p.key_tiles_per_group;
-    const std::int64_t word = head * p.words_per_head + qt * p.words_per_row + (group >> 6);
-    const unsigned bit = static_cast<unsigned>(group & 63);
-    if (p.skip_words && ((p.skip_words[word] >> bit) & 1u)) return 2;
-    if (p.route_words && ((p.route_words[word] >> bit) & 1u)) return 1;
-    return 0;
-}
-
 template <int DC>
 struct Layout {
     static constexpr int kDP = 32 * DC;            // padded head dim, fp16 path
     static constexpr int kD8C = (DC + 1) / 2;      // 64-feature chunks, int8 path
     static constexpr int kDP8 = 64 * kD8C;
     static constexpr int kFB = kDP / 16;           // 16-feature output blocks
-    static constexpr int kKStride = kDP * 2 + 16;  // bytes per K row in LDS
-    static constexpr int kVStride = kDP * 2 + 32;  // bytes per V row in LDS
-    static constexpr int kK8Stride = kDP8 + 16;    // bytes per K8 row in LDS
+    // Row strides pad each row by 16 (K, K8) or 32 (V) bytes so that the
+    // 16 rows an MFMA operand read touches start in distinct LDS banks.
+    static constexpr int kKStride = kDP * 2 + 16;
+    static constexpr int kVStride = kDP * 2 + 32;
+    static constexpr int kK8Stride = kDP8 + 16;
     static constexpr int kKBytes = kTileKeys * kKStride;
     static constexpr int kVBytes = kTileKeys * kVStride;
     static constexpr int kK8Bytes = kTileKeys * kK8Stride;
-    static constexpr int kQ8Stride = kDP8 + 16;    // prologue staging of quantized Q
+    // One buffer_load ... lds per wave moves 1 KiB (64 lanes x 16 bytes).
+    static constexpr int kKLoads = kKBytes / 1024;
+    static constexpr int kVLoads = kVBytes / 1024;
+    static constexpr int kK8Loads = kK8Bytes / 1024;
+    static constexpr int kKPerWave = (kKLoads + kWavesPerGroup - 1) / kWavesPerGroup;
+    static constexpr int kVPerWave = (kVLoads + kWavesPerGroup - 1) / kWavesPerGroup;
+    static constexpr int kK8PerWave = (kK8Loads + kWavesPerGroup - 1) / kWavesPerGroup;
+    static constexpr int kQ8Stride = kDP8 + 16;    // the workgroup's quantized Q rows
+    static constexpr int kQ8Bytes = kRowsPerGroup * kQ8Stride;
     static constexpr int kSmemBytes = kKBytes + kVBytes + kK8Bytes;
-    static_assert(kRowsPerGroup * kQ8Stride <= kSmemBytes, "Q8 staging must fit the tile area");
+    static_assert(kKBytes % 1024 == 0 && kVBytes % 1024 == 0 && kK8Bytes % 1024 == 0,
+                  "tiles are whole wave loads");
 };
 
 __device__ __forceinline__ half8 concat(half4 a, half4 b) {
@@ -115,14 +130,92 @@ __device__ __forceinline__ half4 read_tr16(const unsigned char* lds_byte_address
     return __builtin_bit_cast(half4, raw);
 }
 
-template <int DC, bool kVector, bool kPrecise>
-__global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const AttnParams p) {
+// 16 bytes per lane from buffer offset soffset + voffset into LDS at
+// lds_base + 16 * lane (lds_base is wave-uniform).
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds_base, int voffset,
+                                            int soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds_base), 16, voffset,
+                                             soffset, 0, 0);
+}
+
+// Offset of lane `lane`'s 16-byte piece of wave load `w` of a tile whose LDS
+// rows are `lds_stride` bytes apart: its row and 16-byte column follow from
+// where it lands (lds offset 1024 w + 16 lane). Padding slots and columns at
+// or beyond `row_bytes` (the valid bytes of a global row) read as zero.
+__device__ __forceinline__ int lane_offset(int w, int lane, int lds_stride, int row_bytes, int global_row_bytes) {
+    const int landing = 1024 * w + 16 * lane;
+    const int row = landing / lds_stride;
+    const int column = landing - row * lds_stride;
+    return column < row_bytes ? row * global_row_bytes + column : kOutOfRange;
+}
+
+// Online-softmax state of the two 16-row query blocks a wave owns. Scores
+// enter the softmax as x * c (log2 domain), with c >= 0 folded into the
+// exponent FMA; m is the reference maximum the probabilities are taken
+// against. It is raised lazily - only when a tile's maximum exceeds it by more
+// than kLazyRescale (log2 units) - so most tiles skip the O rescale;
+// probabilities stay <= 2^kLazyRescale, far inside fp16 range. Every
+// probability and the running sum use the same m, so the common factor
+// cancels exactly in O = sum(p v) / sum(p).
+constexpr float kLazyRescale = 8.0f;
+
+template <int kFB>
+struct RowState {
+    float4v o[2][kFB];  // O^T accumulators: lane (g, i) holds O[row i][16fb + 4g + r]
+    float4v l[2];       // row sums (all four entries equal), from a ones-operand MFMA
+    float m[2];
+};
+
+// x[kb] holds the 16 scores of query row i of block b for keys 16kb + 4g + r.
+// c is the per-tile log2-domain factor (>= 0); explicit scores pass c = 1.
+template <int kFB, bool kPrecise>
+__device__ __forceinline__ void softmax_tile(RowState<kFB>& st, int b, float4v (&x)[4], float c,
+                                             half8 (&ph)[2], half8 (&pl)[2]) {
+    float tile = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
+                       fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
+    tile = fmaxf(tile, fmaxf(fmaxf(fmaxf(x[2][0], x[2][1]), fmaxf(x[2][2], x[2][3])),
+                             fmaxf(fmaxf(x[3][0], x[3][1]), fmaxf(x[3][2], x[3][3]))));
+    tile *= c;  // c >= 0 and rounding is monotone: max(x) * c == max(x * c)
+    tile = fmaxf(tile, __shfl_xor(tile, 16));
+    tile = fmaxf(tile, __shfl_xor(tile, 32));
+    const bool raise = tile > st.m[b] + kLazyRescale;
+    if (__any(raise)) {
+        // Rows with no visible key yet keep m = -inf (their sums are still 0).
+        const float m_new = fmaxf(st.m[b], tile);
+        const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(st.m[b] - m_new);
+        st.m[b] = m_new;
+#pragma unroll
+        for (int fb = 0; fb < kFB; ++fb) st.o[b][fb] *= alpha;
+        st.l[b] *= alpha;
+    }
+    // m == -inf only while every score seen, this tile included, is masked.
+    const float neg_m = st.m[b] == -INFINITY ? 0.0f : -st.m[b];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(x[2 * ks][r], c, neg_m));
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[2 * ks + 1][r], c, neg_m));
+            const _Float16 ha = static_cast<_Float16>(a), he = static_cast<_Float16>(e);
+            ph[ks][r] = ha;
+            ph[ks][4 + r] = he;
+            if constexpr (kPrecise) {
+                pl[ks][r] = static_cast<_Float16>(a - static_cast<float>(ha));
+                pl[ks][4 + r] = static_cast<_Float16>(e - static_cast<float>(he));
+            }
+        }
+}
+
+template <int DC, bool kVector, bool kPrecise, bool kDots>
+__global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kernel(const AttnParams p) {
     using L = Layout<DC>;
     constexpr int kDP = L::kDP;
     constexpr int kD8C = L::kD8C;
     constexpr int kFB = L::kFB;
     __shared__ __attribute__((aligned(16))) unsigned char smem[L::kSmemBytes];
-    __shared__ float group_max[kThreadsPerGroup / kWave];
+    // Quantized Q rows (B operand of the INT8 MFMA), read on INT8 tiles only.
+    __shared__ __attribute__((aligned(16))) unsigned char lds_q8[L::kQ8Bytes];
+    __shared__ float group_max[kWavesPerGroup];
     unsigned char* const lds_k = smem;
     unsigned char* const lds_v = smem + L::kKBytes;
     unsigned char* const lds_k8 = smem + L::kKBytes + L::kVBytes;
@@ -133,10 +226,21 @@ __global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const At
     const int g = lane >> 4;
     const int i = lane & 15;
 
-    // Heaviest causal tiles first: block index -> (q block, head).
+    // Block index -> (head, q block). Heads are dealt to XCDs so that the
+    // workgroups sharing a head's K/V run on one XCD's L2; within an XCD a
+    // head's query blocks run together, heaviest causal blocks first.
     const int linear = blockIdx.x;
-    const int qblock = p.causal ? p.q_blocks - 1 - linear / p.heads : linear / p.heads;
-    const std::int64_t head = linear % p.heads;
+    int head32, qslot;
+    if (p.heads % kXcds == 0) {
+        const int xcd = linear % kXcds, slot = linear / kXcds;
+        head32 = xcd + kXcds * (slot / p.q_blocks);
+        qslot = slot % p.q_blocks;
+    } else {
+        head32 = linear / p.q_blocks;
+        qslot = linear % p.q_blocks;
+    }
+    const int qblock = p.causal ? p.q_blocks - 1 - qslot : qslot;
+    const std::int64_t head = head32;
     const int q0 = qblock * kRowsPerGroup;
     const int qw = q0 + wave * kRowsPerWave;
     const int M = p.M, N = p.N, d = p.d;
@@ -144,6 +248,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const At
     const std::uint16_t* Qh = p.Q + head * p.q_stride;
     const std::uint16_t* Kh = p.K + head * p.k_stride;
     const std::uint16_t* Vh = p.V + head * p.v_stride;
+    const std::int8_t* K8h = p.K8 + head * static_cast<std::int64_t>(N) * d;
     float* Oh = p.O + head * p.o_stride;
 
     // ---------------------------------------------------------------- Q
@@ -168,7 +273,6 @@ __global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const At
         }
     }
 
-    int4v q8f[2][kD8C];
     float q_scale = 0.0f;
     if (p.int8_operands) {
         if (p.fuse_q_quant) {
@@ -203,7 +307,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const At
                     packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
                     packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);
                     const int feature = 32 * dc + 8 * g;
-                    *reinterpret_cast<uint2v*>(smem + local * L::kQ8Stride + feature) = packed;
+                    *reinterpret_cast<uint2v*>(lds_q8 + local * L::kQ8Stride + feature) = packed;
                     if (p.q8_out && row < M && feature < d) {
                         std::int8_t* dst = p.q8_out + head * static_cast<std::int64_t>(M) * d +
                                            static_cast<std::int64_t>(row) * d + feature;
@@ -215,26 +319,19 @@ __global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const At
                     }
                 }
             }
-            __syncthreads();
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                const int local = wave * kRowsPerWave + 16 * b + i;
-#pragma unroll
-                for (int m = 0; m < kD8C; ++m)
-                    q8f[b][m] = *reinterpret_cast<const int4v*>(smem + local * L::kQ8Stride + 64 * m + 16 * g);
-            }
-            __syncthreads();  // staging area is reused by the key tiles
         } else {
             q_scale = half_bits_to_float(p.q_scales[head * p.q_blocks + qblock]);
             const std::int8_t* Q8h = p.Q8 + head * static_cast<std::int64_t>(M) * d;
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const int row = qw + 16 * b + i;
+                const int local = wave * kRowsPerWave + 16 * b + i;
+                const int row = q0 + local;
 #pragma unroll
                 for (int m = 0; m < kD8C; ++m) {
                     const int feature = 64 * m + 16 * g;
+                    int4v chunk;
                     if constexpr (kVector) {
-                        q8f[b][m] = (row < M && feature < d)
+                        chunk = (row < M && feature < d)
                             ? *reinterpret_cast<const int4v*>(Q8h + static_cast<std::int64_t>(row) * d + feature)
                             : int4v{0, 0, 0, 0};
                     } else {
@@ -244,114 +341,198 @@ __global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const At
                             bytes[e] = (row < M && feature + e < d)
                                 ? static_cast<unsigned char>(Q8h[static_cast<std::int64_t>(row) * d + feature + e])
                                 : 0;
-                        q8f[b][m] = __builtin_bit_cast(int4v, bytes);
+                        chunk = __builtin_bit_cast(int4v, bytes);
                     }
+                    *reinterpret_cast<int4v*>(lds_q8 + local * L::kQ8Stride + feature) = chunk;
                 }
             }
         }
+        __syncthreads();  // lds_q8 complete
     }
 
-    // ---------------------------------------------------------- key loop
-    float4v o[2][kFB];
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int fb = 0; fb < kFB; ++fb) o[b][fb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run[2] = {-INFINITY, -INFINITY};
-    float l_run[2] = {0.0f, 0.0f};
-
-    const int key_tiles64 = (N - 1) / kTileKeys + 1;
-    int tiles = key_tiles64;
-    if (p.causal) tiles = min(tiles, (q0 + kRowsPerGroup - 1) / kTileKeys + 1);
+    // ------------------------------------------------------ routing masks
+    // Lane c < 16 decodes cell (row c / 2, key half c % 2) of each tile from
+    // the route / skip word it keeps for its query tile; the word is reloaded
+    // only when the tile's group crosses into the next 64-group block. The
+    // ballots make the masks wave-uniform: bit 2r + t <-> cell (r, t).
     const int qt0 = q0 / 16;
-    const std::int64_t trace_base = head * static_cast<std::int64_t>(p.q_tiles16) * p.key_tiles32;
-
-    for (int j = 0; j < tiles; ++j) {
-        const int k0 = j * kTileKeys;
-        // Route codes of the workgroup's 8 x 2 cells: lane c < 16 decodes cell
-        // (row c / 2, key half c % 2); the ballots make the masks wave-uniform.
-        int code = 2;
-        if (lane < 16) code = cell_code(p, head, qt0 + (lane >> 1), 2 * j + (lane & 1));
-        const std::uint32_t int8_mask = static_cast<std::uint32_t>(__ballot(lane < 16 && code == 1));
-        const std::uint32_t skip_mask = static_cast<std::uint32_t>(__ballot(lane < 16 && code == 2));
-        if (p.trace && wave == 0 && lane < 16) {
-            const int qt = qt0 + (lane >> 1), kt = 2 * j + (lane & 1);
-            if (qt < p.q_tiles16 && kt < p.key_tiles32)
-                p.trace[trace_base + static_cast<std::int64_t>(qt) * p.key_tiles32 + kt] =
-                    static_cast<std::uint8_t>(code);
+    const int my_qt = qt0 + ((lane & 15) >> 1);
+    const bool my_row_valid = lane < 16 && my_qt < p.q_tiles16;
+    const std::int64_t my_word_base =
+        head * p.words_per_head + static_cast<std::int64_t>(my_qt) * p.words_per_row;
+    std::int64_t cached_block = -1;
+    std::uint64_t cached_route = 0, cached_skip = 0;
+    auto tile_masks = [&](int j, std::uint32_t& int8_mask, std::uint32_t& skip_mask) {
+        const int kt = 2 * j + (lane & 1);
+        bool skip = true, int8 = false;
+        if (my_row_valid && kt < p.key_tiles32) {
+            const std::int64_t group = kt / p.key_tiles_per_group;
+            const std::int64_t block = group >> 6;
+            if (block != cached_block) {
+                cached_block = block;
+                cached_route = p.route_words ? p.route_words[my_word_base + block] : 0ull;
+                cached_skip = p.skip_words ? p.skip_words[my_word_base + block] : 0ull;
+            }
+            const unsigned bit = static_cast<unsigned>(group & 63);
+            skip = (cached_skip >> bit) & 1u;
+            int8 = !skip && ((cached_route >> bit) & 1u);
         }
-        if (skip_mask == 0xffffu) continue;  // whole 128x64 tile skipped (uniform across the group)
-        const bool need16 = ((~int8_mask & ~skip_mask) & 0xffffu) != 0;
-        const bool need8 = int8_mask != 0;
+        int8_mask = static_cast<std::uint32_t>(__ballot(lane < 16 && int8));
+        skip_mask = static_cast<std::uint32_t>(__ballot(lane < 16 && skip));
+    };
 
-        // ---- cooperative tile loads into LDS
-        if constexpr (kVector) {
-            constexpr int kChunks16 = kDP / 8;  // 16-byte chunks per fp16 row
+    // ------------------------------------------------------ tile movement
+    const std::int64_t kv_bytes = static_cast<std::int64_t>(N) * d * 2;
+    __amdgpu_buffer_rsrc_t rsrc_k = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<std::uint16_t*>(Kh), 0, static_cast<int>(kv_bytes), kBufferFlags);
+    __amdgpu_buffer_rsrc_t rsrc_v = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<std::uint16_t*>(Vh), 0, static_cast<int>(kv_bytes), kBufferFlags);
+    __amdgpu_buffer_rsrc_t rsrc_k8 = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<std::int8_t*>(p.int8_operands ? K8h : p.K8), 0,
+        static_cast<int>(p.int8_operands ? kv_bytes / 2 : 0), kBufferFlags);
+    int off_k[L::kKPerWave], off_v[L::kVPerWave], off_k8[L::kK8PerWave];
+    if constexpr (kVector) {
 #pragma unroll
-            for (int it = 0; it < DC; ++it) {
-                const int c = tid + it * kThreadsPerGroup;
-                const int row = c / kChunks16, col = c % kChunks16;
-                const int key = k0 + row;
-                const bool valid = key < N && col * 8 < d;
-                const std::int64_t offset = static_cast<std::int64_t>(key) * d + col * 8;
-                const uint4v zero{0u, 0u, 0u, 0u};
-                if (need16)
-                    *reinterpret_cast<uint4v*>(lds_k + row * L::kKStride + col * 16) =
-                        valid ? *reinterpret_cast<const uint4v*>(Kh + offset) : zero;
-                *reinterpret_cast<uint4v*>(lds_v + row * L::kVStride + col * 16) =
-                    valid ? *reinterpret_cast<const uint4v*>(Vh + offset) : zero;
+        for (int t = 0; t < L::kKPerWave; ++t)
+            off_k[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kKStride, 2 * d, 2 * d);
+#pragma unroll
+        for (int t = 0; t < L::kVPerWave; ++t)
+            off_v[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kVStride, 2 * d, 2 * d);
+#pragma unroll
+        for (int t = 0; t < L::kK8PerWave; ++t)
+            off_k8[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kK8Stride, d, d);
+    }
+    // K (FP16 cells) and K8 (INT8 cells) of tile j.
+    auto issue_k = [&](int j, bool need16, bool need8) {
+        const int k0 = j * kTileKeys;
+        if constexpr (kVector) {
+            if (need16) {
+#pragma unroll
+                for (int t = 0; t < L::kKPerWave; ++t) {
+                    const int w = wave + kWavesPerGroup * t;
+                    if (w < L::kKLoads) load_to_lds(rsrc_k, lds_k + 1024 * w, off_k[t], k0 * d * 2);
+                }
             }
             if (need8) {
-                const std::int8_t* K8h = p.K8 + head * static_cast<std::int64_t>(N) * d;
-                constexpr int kChunks8 = L::kDP8 / 16;
 #pragma unroll
-                for (int it = 0; it < kD8C; ++it) {
-                    const int c = tid + it * kThreadsPerGroup;
-                    const int row = c / kChunks8, col = c % kChunks8;
-                    const int key = k0 + row;
-                    const bool valid = key < N && col * 16 < d;
-                    *reinterpret_cast<uint4v*>(lds_k8 + row * L::kK8Stride + col * 16) =
-                        valid ? *reinterpret_cast<const uint4v*>(K8h + static_cast<std::int64_t>(key) * d + col * 16)
-                              : uint4v{0u, 0u, 0u, 0u};
+                for (int t = 0; t < L::kK8PerWave; ++t) {
+                    const int w = wave + kWavesPerGroup * t;
+                    if (w < L::kK8Loads) load_to_lds(rsrc_k8, lds_k8 + 1024 * w, off_k8[t], k0 * d);
                 }
             }
         } else {
-            for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
-                const int row = e / kDP, f = e % kDP;
-                const int key = k0 + row;
-                const bool valid = key < N && f < d;
-                const std::int64_t offset = static_cast<std::int64_t>(key) * d + f;
-                if (need16)
-                    *reinterpret_cast<std::uint16_t*>(lds_k + row * L::kKStride + 2 * f) = valid ? Kh[offset] : 0;
-                *reinterpret_cast<std::uint16_t*>(lds_v + row * L::kVStride + 2 * f) = valid ? Vh[offset] : 0;
+            if (need16) {
+                for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
+                    const int row = e / kDP, f = e % kDP, key = k0 + row;
+                    *reinterpret_cast<std::uint16_t*>(lds_k + row * L::kKStride + 2 * f) =
+                        (key < N && f < d) ? Kh[static_cast<std::int64_t>(key) * d + f] : 0;
+                }
             }
             if (need8) {
-                const std::int8_t* K8h = p.K8 + head * static_cast<std::int64_t>(N) * d;
                 for (int e = tid; e < kTileKeys * L::kDP8; e += kThreadsPerGroup) {
-                    const int row = e / L::kDP8, f = e % L::kDP8;
-                    const int key = k0 + row;
+                    const int row = e / L::kDP8, f = e % L::kDP8, key = k0 + row;
                     lds_k8[row * L::kK8Stride + f] =
                         (key < N && f < d) ? static_cast<unsigned char>(K8h[static_cast<std::int64_t>(key) * d + f]) : 0;
                 }
             }
         }
+    };
+    auto issue_v = [&](int j) {
+        const int k0 = j * kTileKeys;
+        if constexpr (kVector) {
+#pragma unroll
+            for (int t = 0; t < L::kVPerWave; ++t) {
+                const int w = wave + kWavesPerGroup * t;
+                if (w < L::kVLoads) load_to_lds(rsrc_v, lds_v + 1024 * w, off_v[t], k0 * d * 2);
+            }
+        } else {
+            for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
+                const int row = e / kDP, f = e % kDP, key = k0 + row;
+                *reinterpret_cast<std::uint16_t*>(lds_v + row * L::kVStride + 2 * f) =
+                    (key < N && f < d) ? Vh[static_cast<std::int64_t>(key) * d + f] : 0;
+            }
+        }
+    };
+    // Own loads complete (vmcnt 0), then the workgroup barrier.
+    auto tile_barrier = [&]() {
+        __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
+    };
+
+    // ---------------------------------------------------------- key loop
+    RowState<kFB> st;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int fb = 0; fb < kFB; ++fb) st.o[b][fb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        st.l[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        st.m[b] = -INFINITY;
+    }
+    const half8 ones{1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
+    const bool positive_scale = p.score_scale >= 0.0f;
+
+    const int key_tiles64 = (N - 1) / kTileKeys + 1;
+    int tiles = key_tiles64;
+    if (p.causal) tiles = min(tiles, (q0 + kRowsPerGroup - 1) / kTileKeys + 1);
+    const std::int64_t trace_base = head * static_cast<std::int64_t>(p.q_tiles16) * p.key_tiles32;
+    auto write_trace = [&](int j, std::uint32_t int8_mask, std::uint32_t skip_mask) {
+        if (wave == 0 && lane < 16) {
+            const int qt = qt0 + (lane >> 1), kt = 2 * j + (lane & 1);
+            if (qt < p.q_tiles16 && kt < p.key_tiles32)
+                p.trace[trace_base + static_cast<std::int64_t>(qt) * p.key_tiles32 + kt] =
+                    static_cast<std::uint8_t>(((skip_mask >> lane) & 1u) ? 2u : ((int8_mask >> lane) & 1u));
+        }
+    };
+    auto needs16 = [](std::uint32_t int8_mask, std::uint32_t skip_mask) {
+        return ((~int8_mask & ~skip_mask) & 0xffffu) != 0;
+    };
+
+    // Tiles whose 16 cells are all skipped are stepped over: next_tile(j)
+    // returns the first tile >= j with a visible cell (or `tiles`) and its
+    // masks, writing the routing trace of the tiles it passes.
+    std::uint32_t cur_int8 = 0, cur_skip = 0;
+    auto next_tile = [&](int j) {
+        for (; j < tiles; ++j) {
+            tile_masks(j, cur_int8, cur_skip);
+            if (kDots && p.trace) write_trace(j, cur_int8, cur_skip);
+            if (cur_skip != 0xffffu) break;
+        }
+        return j;
+    };
+    int j = next_tile(0);
+    if (j < tiles) issue_k(j, needs16(cur_int8, cur_skip), cur_int8 != 0);
+
+    // One iteration per visible tile; the accumulator update at its end runs
+    // on every wave (inactive waves add zero probabilities), which keeps the
+    // O / l / m state on a single straight-line path through the loop.
+    while (j < tiles) {
+        const int k0 = j * kTileKeys;
+        const std::uint32_t int8_mask = cur_int8, skip_mask = cur_skip;
+        tile_barrier();  // K_j landed; every wave finished P.V of the previous tile
+        issue_v(j);
 
         const unsigned wave_int8 = (int8_mask >> (4 * wave)) & 0xfu;
         const unsigned wave_skip = (skip_mask >> (4 * wave)) & 0xfu;
-        const bool wave_active = qw < M && wave_skip != 0xfu && !(p.causal && k0 > qw + kRowsPerWave - 1);
-        if (wave_active) {
+        const bool active = qw < M && wave_skip != 0xfu && !(p.causal && k0 > qw + kRowsPerWave - 1);
+        // Tiles needing no element mask and a non-negative scale use the fast
+        // path: raw MFMA results go straight into the exponent FMA.
+        const bool masked = k0 + kTileKeys > N || (p.causal && k0 + kTileKeys - 1 > qw);
+        const bool fast = positive_scale && !masked;
+
+        float4v s[2][4];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) s[b][kb] = float4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        float c = 1.0f;
+        if (active) {
             float k_factor = 0.0f;  // q_scale * k_scale * score_scale * log2(e)
             if (wave_int8) {
                 const float k_scale = half_bits_to_float(p.k_scales[head * p.k_blocks + j]);
                 k_factor = ((q_scale * k_scale) * p.score_scale) * kLog2e;
             }
-            const float f_factor = p.score_log2;
-
             // ---- scores S^T[kb][b]: lane (g, i) holds query i, keys 16kb + 4g + r
-            float4v s[2][4];
-            const bool uniform16 = wave_int8 == 0 && wave_skip == 0;
-            if (uniform16) {
+            auto fp16_scores = [&]() {
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb) {
                     float4v acc0{0.0f, 0.0f, 0.0f, 0.0f}, acc1{0.0f, 0.0f, 0.0f, 0.0f};
@@ -362,56 +543,117 @@ __global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const At
                         acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][dc], acc0, 0, 0, 0);
                         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[1][dc], acc1, 0, 0, 0);
                     }
-                    s[0][kb] = acc0 * f_factor;
-                    s[1][kb] = acc1 * f_factor;
+                    s[0][kb] = acc0;
+                    s[1][kb] = acc1;
+                    // Keep the scheduler from hoisting every K fragment read
+                    // of the tile (register pressure); the co-resident
+                    // workgroup hides the LDS latency instead.
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-            } else {
+            };
+            // The wave's quantized Q rows, loaded on tiles that have INT8 cells.
+            int4v q8f[2][kD8C];
+            auto load_q8 = [&]() {
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int m = 0; m < kD8C; ++m)
+                        q8f[b][m] = *reinterpret_cast<const int4v*>(
+                            lds_q8 + (wave * kRowsPerWave + 16 * b + i) * L::kQ8Stride + 64 * m + 16 * g);
+            };
+            // Exact int32 dots of key block kb for both query blocks.
+            auto int8_dots = [&](int kb, int4v& acc0, int4v& acc1) {
+                acc0 = int4v{0, 0, 0, 0};
+                acc1 = int4v{0, 0, 0, 0};
+#pragma unroll
+                for (int m = 0; m < kD8C; ++m) {
+                    const int4v kf = *reinterpret_cast<const int4v*>(
+                        lds_k8 + (16 * kb + i) * L::kK8Stride + 64 * m + 16 * g);
+                    acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, q8f[0][m], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, q8f[1][m], acc1, 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            // Raw int32 dots of INT8 cells (verification output).
+            auto store_dots = [&](int kb, int b, const int4v& acc) {
+                const int query = qw + 16 * b + i;
+                std::int32_t* row = p.dots + head * static_cast<std::int64_t>(M) * N +
+                                    static_cast<std::int64_t>(query) * N;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 16 * kb + 4 * g + r;
+                    if (query < M && key < N && !(p.causal && key > query)) row[key] = acc[r];
+                }
+            };
+            if (wave_skip == 0 && wave_int8 == 0) {
+                fp16_scores();
+                c = p.score_log2;
+            } else if (wave_skip == 0 && wave_int8 == 0xfu) {
+                load_q8();
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb) {
-                    const int t = kb >> 1;
+                    int4v acc0, acc1;
+                    int8_dots(kb, acc0, acc1);
+                    if (kDots && p.dots) {
+                        store_dots(kb, 0, acc0);
+                        store_dots(kb, 1, acc1);
+                    }
 #pragma unroll
-                    for (int b = 0; b < 2; ++b) {
-                        const unsigned cell = 2 * b + t;
-                        const bool skip = (wave_skip >> cell) & 1u;
-                        const bool int8 = (wave_int8 >> cell) & 1u;
-                        if (skip) {
-                            s[b][kb] = float4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-                        } else if (int8) {
-                            int4v acc{0, 0, 0, 0};
+                    for (int r = 0; r < 4; ++r) {
+                        s[0][kb][r] = static_cast<float>(acc0[r]);
+                        s[1][kb][r] = static_cast<float>(acc1[r]);
+                    }
+                }
+                c = k_factor;
+            } else {
+                // Mixed routes inside the wave: both score kinds where present,
+                // explicitly scaled, then selected per cell (bit 2b + kb/2).
+                const unsigned wave_fp16 = ~(wave_int8 | wave_skip) & 0xfu;
+                if (wave_fp16) {
+                    fp16_scores();
 #pragma unroll
-                            for (int m = 0; m < kD8C; ++m) {
-                                const int4v kf = *reinterpret_cast<const int4v*>(
-                                    lds_k8 + (16 * kb + i) * L::kK8Stride + 64 * m + 16 * g);
-                                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, q8f[b][m], acc, 0, 0, 0);
-                            }
-                            if (p.dots) {
-                                const int query = qw + 16 * b + i;
+                    for (int b = 0; b < 2; ++b)
 #pragma unroll
-                                for (int r = 0; r < 4; ++r) {
-                                    const int key = k0 + 16 * kb + 4 * g + r;
-                                    if (query < M && key < N && !(p.causal && key > query))
-                                        p.dots[head * static_cast<std::int64_t>(M) * N +
-                                               static_cast<std::int64_t>(query) * N + key] = acc[r];
-                                }
-                            }
+                        for (int kb = 0; kb < 4; ++kb) s[b][kb] *= p.score_log2;
+                } else {
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) s[b][kb][r] = static_cast<float>(acc[r]) * k_factor;
-                        } else {
-                            float4v acc{0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int b = 0; b < 2; ++b)
 #pragma unroll
-                            for (int dc = 0; dc < DC; ++dc) {
-                                const half8 kf = *reinterpret_cast<const half8*>(
-                                    lds_k + (16 * kb + i) * L::kKStride + (32 * dc + 8 * g) * 2);
-                                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[b][dc], acc, 0, 0, 0);
-                            }
-                            s[b][kb] = acc * f_factor;
+                        for (int kb = 0; kb < 4; ++kb) s[b][kb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+                if (wave_int8) {
+                    load_q8();
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb) {
+                        int4v acc[2];
+                        int8_dots(kb, acc[0], acc[1]);
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) {
+                            const bool cell_int8 = (wave_int8 >> (2 * b + (kb >> 1))) & 1u;
+                            if (kDots && p.dots && cell_int8) store_dots(kb, b, acc[b]);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                s[b][kb][r] = cell_int8 ? static_cast<float>(acc[b][r]) * k_factor : s[b][kb][r];
                         }
                     }
                 }
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+                        if ((wave_skip >> (2 * b + (kb >> 1))) & 1u)
+                            s[b][kb] = float4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+                c = 1.0f;
             }
-
-            // ---- element masks: key tail and causal diagonal
-            if (k0 + kTileKeys > N || (p.causal && k0 + kTileKeys - 1 > qw)) {
+            if (!fast && c != 1.0f) {
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb) s[b][kb] *= c;
+                c = 1.0f;
+            }
+            // ---- element masks: key tail and causal diagonal (explicit scores)
+            if (masked) {
 #pragma unroll
                 for (int b = 0; b < 2; ++b) {
                     const int query = qw + 16 * b + i;
@@ -424,84 +666,54 @@ __global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const At
                         }
                 }
             }
+        }
 
-            // ---- online softmax (log2 domain) and P.V
-            half8 ph[2][2];
-            half8 pl[2][2];
+        tile_barrier();  // V_j landed; every wave finished reading K_j
+        const int j_next = next_tile(j + 1);
+        if (j_next < tiles) issue_k(j_next, needs16(cur_int8, cur_skip), cur_int8 != 0);
+
+        // ---- online softmax, then O^T += V^T P^T and l += 1^T P^T
+        half8 ph[2][2], pl[2][2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) softmax_tile<kFB, kPrecise>(st, b, s[b], c, ph[b], pl[b]);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const unsigned char* v_lo = lds_v + (32 * ks + 4 * g + (i >> 2)) * L::kVStride + 8 * (i & 3);
+            const unsigned char* v_hi = v_lo + 16 * L::kVStride;
+#pragma unroll
+            for (int fb = 0; fb < kFB; ++fb) {
+                const half8 vf = concat(read_tr16(v_lo + 32 * fb), read_tr16(v_hi + 32 * fb));
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    st.o[b][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[b][ks], st.o[b][fb], 0, 0, 0);
+                    if constexpr (kPrecise)
+                        st.o[b][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[b][ks], st.o[b][fb], 0, 0, 0);
+                }
+                if (fb % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                float tile_max = -INFINITY;
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) tile_max = fmaxf(tile_max, s[b][kb][r]);
-                tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
-                tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-                const float m_new = fmaxf(m_run[b], tile_max);
-                const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-                const float alpha = __builtin_amdgcn_exp2f(m_run[b] - m_use);
-                m_run[b] = m_new;
-                float sum = 0.0f;
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float pr = __builtin_amdgcn_exp2f(s[b][kb][r] - m_use);
-                        s[b][kb][r] = pr;
-                        sum += pr;
-                    }
-                l_run[b] = l_run[b] * alpha + sum;
-#pragma unroll
-                for (int fb = 0; fb < kFB; ++fb) o[b][fb] *= alpha;
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float a = s[b][2 * ks][r], c = s[b][2 * ks + 1][r];
-                        const _Float16 ha = static_cast<_Float16>(a), hc = static_cast<_Float16>(c);
-                        ph[b][ks][r] = ha;
-                        ph[b][ks][4 + r] = hc;
-                        if constexpr (kPrecise) {
-                            pl[b][ks][r] = static_cast<_Float16>(a - static_cast<float>(ha));
-                            pl[b][ks][4 + r] = static_cast<_Float16>(c - static_cast<float>(hc));
-                        }
-                    }
-            }
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const unsigned char* v_lo = lds_v + (32 * ks + 4 * g + (i >> 2)) * L::kVStride + 8 * (i & 3);
-                const unsigned char* v_hi = v_lo + 16 * L::kVStride;
-#pragma unroll
-                for (int fb = 0; fb < kFB; ++fb) {
-                    const half8 vf = concat(read_tr16(v_lo + 32 * fb), read_tr16(v_hi + 32 * fb));
-#pragma unroll
-                    for (int b = 0; b < 2; ++b) {
-                        o[b][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[b][ks], o[b][fb], 0, 0, 0);
-                        if constexpr (kPrecise)
-                            o[b][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[b][ks], o[b][fb], 0, 0, 0);
-                    }
-                }
+                st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph[b][ks], st.l[b], 0, 0, 0);
+                if constexpr (kPrecise)
+                    st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pl[b][ks], st.l[b], 0, 0, 0);
             }
         }
-        __syncthreads();
+        j = j_next;
     }
 
     // Routing trace of tiles a causal workgroup never visits.
-    if (p.trace && wave == 0 && lane < 16) {
+    if (kDots && p.trace && tiles < key_tiles64) {
         for (int j = tiles; j < key_tiles64; ++j) {
-            const int qt = qt0 + (lane >> 1), kt = 2 * j + (lane & 1);
-            if (qt < p.q_tiles16 && kt < p.key_tiles32)
-                p.trace[trace_base + static_cast<std::int64_t>(qt) * p.key_tiles32 + kt] =
-                    static_cast<std::uint8_t>(cell_code(p, head, qt, kt));
+            std::uint32_t int8_mask = 0, skip_mask = 0;
+            tile_masks(j, int8_mask, skip_mask);
+            write_trace(j, int8_mask, skip_mask);
         }
     }
 
     // ---------------------------------------------------------- epilogue
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-        float l = l_run[b];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+        const float l = st.l[b][0];
         const float inverse = l > 0.0f ? 1.0f / l : 0.0f;
         const int row = qw + 16 * b + i;
         if (row >= M) continue;
@@ -509,7 +721,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const At
 #pragma unroll
         for (int fb = 0; fb < kFB; ++fb) {
             const int feature = 16 * fb + 4 * g;
-            const float4v value = o[b][fb] * inverse;
+            const float4v value = st.o[b][fb] * inverse;
             if constexpr (kVector) {
                 if (feature < d) *reinterpret_cast<float4v*>(out_row + feature) = value;
             } else {
@@ -521,18 +733,24 @@ __global__ __launch_bounds__(kThreadsPerGroup, 2) void attention_kernel(const At
     }
 }
 
-template <int DC, bool kVector, bool kPrecise>
+template <int DC, bool kVector, bool kPrecise, bool kDots>
 hipError_t launch_variant(const AttnParams& p, hipStream_t stream) {
     const unsigned blocks = static_cast<unsigned>(p.q_blocks) * static_cast<unsigned>(p.heads);
-    attention_kernel<DC, kVector, kPrecise><<<blocks, kThreadsPerGroup, 0, stream>>>(p);
+    attention_kernel<DC, kVector, kPrecise, kDots><<<blocks, kThreadsPerGroup, 0, stream>>>(p);
     return hipGetLastError();
+}
+
+template <int DC, bool kVector>
+hipError_t launch_vp(const AttnParams& p, bool precise, bool dots, hipStream_t stream) {
+    if (precise)
+        return dots ? launch_variant<DC, kVector, true, true>(p, stream) : launch_variant<DC, kVector, true, false>(p, stream);
+    return dots ? launch_variant<DC, kVector, false, true>(p, stream) : launch_variant<DC, kVector, false, false>(p, stream);
 }
 
 template <int DC>
 hipError_t launch_dc(const AttnParams& p, bool vector, bool precise, hipStream_t stream) {
-    if (vector)
-        return precise ? launch_variant<DC, true, true>(p, stream) : launch_variant<DC, true, false>(p, stream);
-    return precise ? launch_variant<DC, false, true>(p, stream) : launch_variant<DC, false, false>(p, stream);
+    const bool dots = p.dots != nullptr || p.trace != nullptr;
+    return vector ? launch_vp<DC, true>(p, precise, dots, stream) : launch_vp<DC, false>(p, precise, dots, stream);
 }
 
 bool aligned(const void* pointer, std::size_t bytes) {
@@ -575,9 +793,12 @@ hipError_t launch_attention(const AttnParams& p, bool precise, hipStream_t strea
     if (static_cast<long long>(p.q_blocks) * p.heads > 0x7fffffffLL) return hipErrorInvalidConfiguration;
     hipError_t status = check_device();
     if (status != hipSuccess) return status;
+    // The vector path moves 16-byte pieces and addresses a head's K / V with
+    // 32-bit buffer offsets; other shapes take the element-wise path.
     bool vector = p.d % 16 == 0 && aligned(p.Q, 16) && aligned(p.K, 16) && aligned(p.V, 16) &&
                   aligned(p.O, 16) && p.q_stride % 8 == 0 && p.k_stride % 8 == 0 &&
-                  p.v_stride % 8 == 0 && p.o_stride % 4 == 0;
+                  p.v_stride % 8 == 0 && p.o_stride % 4 == 0 &&
+                  static_cast<std::int64_t>(p.N) * p.d * 2 < (std::int64_t{1} << 31);
     if (p.int8_operands) {
         if (!p.fuse_q_quant) vector = vector && aligned(p.Q8, 16);
         if (p.q8_out) vector = vector && aligned(p.q8_out, 8);

@@ -2,6 +2,7 @@
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Any, Optional
@@ -23,7 +24,9 @@ class TileMixError(RuntimeError):
 
 
 def library_path() -> Path:
-    return _PACKAGE_DIR / _LIB_NAME
+    """The in-tree build, or the file named by TILEMIX_HIP_LIBRARY (an alternative build)."""
+    override = os.environ.get("TILEMIX_HIP_LIBRARY")
+    return Path(override) if override else _PACKAGE_DIR / _LIB_NAME
 
 
 class _BatchedArgs(ctypes.Structure):
