@@ -51,6 +51,9 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline work")
     p.add_argument("--check-rows", type=int, default=4096)
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="after timing, run one device copy of this many MiB on the bench stream "
+                        "(calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE against known bytes)")
     return p.parse_args()
 
 
@@ -114,6 +117,14 @@ def main() -> int:
             step(pairs[k])
         torch.cuda.synchronize()
         t1 = time.perf_counter()
+        if args.copy_probe_mib > 0:
+            src = torch.ones(args.copy_probe_mib << 19, dtype=torch.float16, device=dev)
+            dst = torch.empty_like(src)
+            torch.cuda.synchronize()
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            log(f"copy probe: {args.copy_probe_mib} MiB read + {args.copy_probe_mib} MiB written")
+            del src, dst
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     attn_ms = float(np.mean([a.elapsed_time(b) for a, b in pairs]))
     log(f"step {ms_per_step:.4f} ms, attention kernel {attn_ms:.4f} ms (HIP events)")
@@ -155,9 +166,16 @@ def main() -> int:
             "frac": round(achieved / blended_peak, 4),
             "traffic": None,
             "kernel_ms": round(attn_ms, 5),
+            "achieved_hbm_gbs": None,
             "peak_basis": "blended: ops_int8/5033.2T + flops_fp16/2516.6T",
         },
     }
+
+    measured = measured_traffic(w.describe())
+    if measured is not None:
+        result["roofline"]["traffic"] = measured["traffic_bytes"]
+        result["roofline"]["achieved_hbm_gbs"] = round(measured["traffic_bytes"] / (attn_ms * 1e-3) / 1e9, 1)
+        result["roofline"]["traffic_source"] = measured["source"]
 
     if not args.no_check:
         result["parity"] = parity_check(w, Q, K, V, O, K8, k_scales, codes, args)
@@ -169,6 +187,16 @@ def main() -> int:
 
     print(json.dumps(result), flush=True)
     return 0
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per attention launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE
+    (calibrated on a copy of known size) for this workload, if recorded."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    entry = json.loads(path.read_text()).get("attention_kernel")
+    return entry if entry and entry.get("workload") == workload else None
 
 
 def parity_check(w, Q, K, V, O, K8, k_scales, codes, args) -> dict:

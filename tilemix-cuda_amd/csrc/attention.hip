@@ -233,8 +233,17 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     int head32, qslot;
     if (p.heads % kXcds == 0) {
         const int xcd = linear % kXcds, slot = linear / kXcds;
-        head32 = xcd + kXcds * (slot / p.q_blocks);
-        qslot = slot % p.q_blocks;
+        const int heads_per_xcd = p.heads / kXcds;
+        if (p.causal) {
+            head32 = xcd + kXcds * (slot % heads_per_xcd);
+            qslot = slot / heads_per_xcd;
+        } else {
+            head32 = xcd + kXcds * (slot / p.q_blocks);
+            qslot = slot % p.q_blocks;
+        }
+    } else if (p.causal) {
+        head32 = linear % p.heads;
+        qslot = linear / p.heads;
     } else {
         head32 = linear / p.q_blocks;
         qslot = linear % p.q_blocks;
