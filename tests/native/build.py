@@ -1,0 +1,46 @@
+"""Build the native test driver tests/native/_build/tilemix_test.
+
+It restates src/tests/tilemix_test.cu against the HIP library's C++ API
+(include/attention_fused.h) and links the C oracle as its checker; build the
+library first (tilemix-cuda_amd/build.py).
+
+Usage: python tests/native/build.py
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent.parent
+OUT = HERE / "_build"
+EXE = OUT / "tilemix_test"
+HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
+
+
+def _run(cmd: list[str]) -> None:
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"command failed ({result.returncode}): {' '.join(cmd)}\n{result.stderr}{result.stdout}")
+
+
+def build() -> Path:
+    OUT.mkdir(parents=True, exist_ok=True)
+    oracle_obj = OUT / "tilemix_oracle.o"
+    _run(["gcc", "-O2", "-std=c99", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
+          "-c", str(ROOT / "oracle" / "tilemix_oracle.c"), "-o", str(oracle_obj)])
+    test_obj = OUT / "tilemix_test.o"
+    _run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", f"-I{ROOT / 'include'}", f"-I{ROOT / 'oracle'}",
+          "-Wno-unused-command-line-argument", "-c", str(HERE / "tilemix_test.cpp"), "-o", str(test_obj)])
+    tmp = EXE.with_suffix(".tmp")
+    _run([HIPCC, "--offload-arch=gfx950", str(test_obj), str(oracle_obj), "-fopenmp",
+          f"-L{ROOT / 'tilemix-cuda_amd'}", "-ltilemix_hip", "-Wl,-rpath,$ORIGIN/../../../tilemix-cuda_amd",
+          "-o", str(tmp)])
+    os.replace(tmp, EXE)
+    return EXE
+
+
+if __name__ == "__main__":
+    print(f"built {build()}")

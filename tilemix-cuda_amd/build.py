@@ -1,9 +1,8 @@
-"""Build the gfx950 TileMix library and its native drivers with hipcc.
+"""Build the gfx950 TileMix library and its demo driver with hipcc.
 
 Outputs (in-tree, git-ignored, shipped with the tree to the GPU host):
   tilemix-cuda_amd/libtilemix_hip.so        the library (C ABI of include/tilemix_capi.h)
   tilemix-cuda_amd/_build/tilemix_demo      demo driver (restates the reference src/main.cu)
-  tests/native/_build/tilemix_test          native test driver (restates src/tests/tilemix_test.cu)
 
 Usage: python tilemix-cuda_amd/build.py [--lib-only] [--jobs N]
 """
@@ -23,10 +22,7 @@ CSRC = PACKAGE / "csrc"
 INCLUDE = ROOT / "include"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libtilemix_hip.so"
-NATIVE_TEST_DIR = ROOT / "tests" / "native"
-NATIVE_TEST = NATIVE_TEST_DIR / "_build" / "tilemix_test"
 DEMO = BUILD / "tilemix_demo"
-ORACLE_DIR = ROOT / "oracle"
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -78,27 +74,6 @@ def build_library(jobs: int) -> Path:
     return LIBRARY
 
 
-def build_oracle() -> None:
-    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
-
-
-def build_native_test() -> Path:
-    """tests/native/tilemix_test.cpp links the library and (as its checker) the oracle."""
-    NATIVE_TEST.parent.mkdir(parents=True, exist_ok=True)
-    oracle_obj = NATIVE_TEST.parent / "tilemix_oracle.o"
-    _run(["gcc", "-O2", "-std=c99", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
-          "-c", str(ORACLE_DIR / "tilemix_oracle.c"), "-o", str(oracle_obj)])
-    test_obj = NATIVE_TEST.parent / "tilemix_test.o"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", f"-I{INCLUDE}", f"-I{ORACLE_DIR}",
-          "-Wno-unused-command-line-argument", "-c", str(NATIVE_TEST_DIR / "tilemix_test.cpp"),
-          "-o", str(test_obj)])
-    tmp = NATIVE_TEST.with_suffix(".tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", str(test_obj), str(oracle_obj), "-fopenmp",
-          f"-L{PACKAGE}", "-ltilemix_hip", "-Wl,-rpath,$ORIGIN/../../../tilemix-cuda_amd", "-o", str(tmp)])
-    os.replace(tmp, NATIVE_TEST)
-    return NATIVE_TEST
-
-
 def build_demo() -> Path:
     obj = BUILD / "demo_main.o"
     _run([HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", f"-I{INCLUDE}",
@@ -115,8 +90,6 @@ def build_all(lib_only: bool = False, jobs: int | None = None) -> None:
     build_library(jobs)
     if lib_only:
         return
-    build_oracle()
-    build_native_test()
     build_demo()
 
 
