@@ -44,6 +44,7 @@ DEVICE_FLAGS = [
 ]
 
 LIB_SOURCES = ["quantize.hip", "attention.hip"]
+SOURCE_FLAGS: dict[str, list[str]] = {}
 
 
 def _run(cmd: list[str]) -> None:
@@ -60,7 +61,8 @@ def _run(cmd: list[str]) -> None:
 
 def compile_object(source: Path, obj: Path) -> Path:
     obj.parent.mkdir(parents=True, exist_ok=True)
-    _run([HIPCC, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(source), "-o", str(obj)])
+    _run([HIPCC, *DEVICE_FLAGS, *SOURCE_FLAGS.get(source.name, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(source),
+          "-o", str(obj)])
     return obj
 
 

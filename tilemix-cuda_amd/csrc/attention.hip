@@ -17,8 +17,9 @@
 //    v_mfma_f32_16x16x32_f16; the V^T operand is read from the row-major V
 //    tile in LDS with ds_read_b64_tr_b16, which transposes 16-bit elements
 //    across each 16-lane group. Key order inside a 32-key MFMA step is
-//    permuted identically on both operands. Row sums come from the same
-//    MFMA with an all-ones operand.
+//    permuted identically on both operands. Row sums add exactly the fp16
+//    probabilities P.V uses (v_dot2_f32_f16 against 1), per lane, reduced
+//    over the row's lanes once at the end.
 //  * K, K8 and V tiles move HBM -> LDS with buffer_load ... lds (no VGPR
 //    staging): per-lane offsets into the padded, bank-conflict-free LDS rows
 //    are computed once, each tile only changes a scalar offset, and rows past
@@ -30,8 +31,7 @@
 //  * The optional in-kernel Q quantization reproduces quantize_tilemix_qk's
 //    bytes exactly: the workgroup's 128 rows are exactly one Q block.
 
-#include "tilemix_device.h"
-#include "tilemix_launch.h"
+#include "attention_common.h"
 #include "tilemix_capi.h"
 
 #include <atomic>
@@ -45,53 +45,11 @@ constexpr int kThreadsPerGroup = 256;
 constexpr int kWavesPerGroup = kThreadsPerGroup / kWave;
 constexpr int kRowsPerGroup = 128;  // one Q quantization block
 constexpr int kRowsPerWave = 32;
-constexpr int kTileKeys = 64;  // one K quantization block
 #ifndef TILEMIX_GROUPS_PER_CU
 #define TILEMIX_GROUPS_PER_CU 2
 #endif
 // Workgroups per CU the register allocation is sized for (launch bound).
 constexpr int kGroupsPerCU = TILEMIX_GROUPS_PER_CU;
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kXcds = 8;                        // MI355X: 8 XCDs, workgroups dealt round-robin
-constexpr std::uint32_t kBufferFlags = 0x00020000u;  // raw buffer resource word 3, gfx9 family
-constexpr int kOutOfRange = static_cast<int>(0x80000000u);  // buffer offset that reads as zero
-
-struct AttnParams {
-    const std::uint16_t* Q;
-    const std::uint16_t* K;
-    const std::uint16_t* V;
-    float* O;
-    const std::int8_t* Q8;
-    const std::int8_t* K8;
-    const std::uint16_t* q_scales;
-    const std::uint16_t* k_scales;
-    const std::uint64_t* route_words;
-    const std::uint64_t* skip_words;
-    std::uint8_t* trace;
-    std::int32_t* dots;
-    std::int8_t* q8_out;
-    std::uint16_t* q_scales_out;
-    std::int64_t q_stride;
-    std::int64_t k_stride;
-    std::int64_t v_stride;
-    std::int64_t o_stride;
-    std::int64_t words_per_row;
-    std::int64_t words_per_head;
-    int heads;
-    int M;
-    int N;
-    int d;
-    int key_tiles_per_group;
-    int q_tiles16;
-    int key_tiles32;
-    int q_blocks;
-    int k_blocks;
-    int causal;
-    int fuse_q_quant;
-    int int8_operands;
-    float score_log2;  // score_scale * log2(e)
-    float score_scale;
-};
 
 template <int DC>
 struct Layout {
@@ -121,48 +79,12 @@ struct Layout {
                   "tiles are whole wave loads");
 };
 
-__device__ __forceinline__ half8 concat(half4 a, half4 b) {
-    return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-
-__device__ __forceinline__ half4 read_tr16(const unsigned char* lds_byte_address) {
-    const short4v raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(lds_byte_address));
-    return __builtin_bit_cast(half4, raw);
-}
-
-// 16 bytes per lane from buffer offset soffset + voffset into LDS at
-// lds_base + 16 * lane (lds_base is wave-uniform).
-__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds_base, int voffset,
-                                            int soffset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds_base), 16, voffset,
-                                             soffset, 0, 0);
-}
-
-// Offset of lane `lane`'s 16-byte piece of wave load `w` of a tile whose LDS
-// rows are `lds_stride` bytes apart: its row and 16-byte column follow from
-// where it lands (lds offset 1024 w + 16 lane). Padding slots and columns at
-// or beyond `row_bytes` (the valid bytes of a global row) read as zero.
-__device__ __forceinline__ int lane_offset(int w, int lane, int lds_stride, int row_bytes, int global_row_bytes) {
-    const int landing = 1024 * w + 16 * lane;
-    const int row = landing / lds_stride;
-    const int column = landing - row * lds_stride;
-    return column < row_bytes ? row * global_row_bytes + column : kOutOfRange;
-}
-
-// Online-softmax state of the two 16-row query blocks a wave owns. Scores
-// enter the softmax as x * c (log2 domain), with c >= 0 folded into the
-// exponent FMA; m is the reference maximum the probabilities are taken
-// against. It is raised lazily - only when a tile's maximum exceeds it by more
-// than kLazyRescale (log2 units) - so most tiles skip the O rescale;
-// probabilities stay <= 2^kLazyRescale, far inside fp16 range. Every
-// probability and the running sum use the same m, so the common factor
-// cancels exactly in O = sum(p v) / sum(p).
-constexpr float kLazyRescale = 8.0f;
-
+// Online-softmax state of the two 16-row query blocks a wave owns (scores in
+// the log2 domain, m raised lazily; see kLazyRescale).
 template <int kFB>
 struct RowState {
     float4v o[2][kFB];  // O^T accumulators: lane (g, i) holds O[row i][16fb + 4g + r]
-    float4v l[2];       // row sums (all four entries equal), from a ones-operand MFMA
+    float l[2];         // this lane's share of the row sum (its keys)
     float m[2];
 };
 
@@ -204,6 +126,18 @@ __device__ __forceinline__ void softmax_tile(RowState<kFB>& st, int b, float4v (
                 pl[ks][4 + r] = static_cast<_Float16>(e - static_cast<float>(he));
             }
         }
+    // Row sum of exactly the fp16 probabilities P.V uses (exact fp32 sums of
+    // pairs, v_dot2_f32_f16 against 1), so the rounding of P cancels in O.
+    const half2v one2{1.0f16, 1.0f16};
+    float sum = st.l[b];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+            sum = __builtin_amdgcn_fdot2(half2v{ph[ks][k], ph[ks][k + 1]}, one2, sum, false);
+            if constexpr (kPrecise) sum = __builtin_amdgcn_fdot2(half2v{pl[ks][k], pl[ks][k + 1]}, one2, sum, false);
+        }
+    st.l[b] = sum;
 }
 
 template <int DC, bool kVector, bool kPrecise, bool kDots>
@@ -226,29 +160,8 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     const int g = lane >> 4;
     const int i = lane & 15;
 
-    // Block index -> (head, q block). Heads are dealt to XCDs so that the
-    // workgroups sharing a head's K/V run on one XCD's L2; within an XCD a
-    // head's query blocks run together, heaviest causal blocks first.
-    const int linear = blockIdx.x;
-    int head32, qslot;
-    if (p.heads % kXcds == 0) {
-        const int xcd = linear % kXcds, slot = linear / kXcds;
-        const int heads_per_xcd = p.heads / kXcds;
-        if (p.causal) {
-            head32 = xcd + kXcds * (slot % heads_per_xcd);
-            qslot = slot / heads_per_xcd;
-        } else {
-            head32 = xcd + kXcds * (slot / p.q_blocks);
-            qslot = slot % p.q_blocks;
-        }
-    } else if (p.causal) {
-        head32 = linear % p.heads;
-        qslot = linear / p.heads;
-    } else {
-        head32 = linear / p.q_blocks;
-        qslot = linear % p.q_blocks;
-    }
-    const int qblock = p.causal ? p.q_blocks - 1 - qslot : qslot;
+    int head32, qblock;
+    map_block(blockIdx.x, p.heads, p.q_blocks, p.causal != 0, head32, qblock);
     const std::int64_t head = head32;
     const int q0 = qblock * kRowsPerGroup;
     const int qw = q0 + wave * kRowsPerWave;
@@ -474,10 +387,9 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
         for (int fb = 0; fb < kFB; ++fb) st.o[b][fb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-        st.l[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        st.l[b] = 0.0f;
         st.m[b] = -INFINITY;
     }
-    const half8 ones{1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
     const bool positive_scale = p.score_scale >= 0.0f;
 
     const int key_tiles64 = (N - 1) / kTileKeys + 1;
@@ -700,12 +612,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 }
                 if (fb % 2 == 1) __builtin_amdgcn_sched_barrier(0);
             }
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph[b][ks], st.l[b], 0, 0, 0);
-                if constexpr (kPrecise)
-                    st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pl[b][ks], st.l[b], 0, 0, 0);
-            }
+
         }
         j = j_next;
     }
@@ -722,7 +629,9 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     // ---------------------------------------------------------- epilogue
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-        const float l = st.l[b][0];
+        float l = st.l[b];
+        l += __shfl_xor(l, 16);  // the row's four lanes: i, i + 16, i + 32, i + 48
+        l += __shfl_xor(l, 32);
         const float inverse = l > 0.0f ? 1.0f / l : 0.0f;
         const int row = qw + 16 * b + i;
         if (row >= M) continue;

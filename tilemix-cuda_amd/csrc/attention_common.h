@@ -1,0 +1,137 @@
+#pragma once
+// Definitions of the attention kernel (attention.hip) kept apart from it:
+// launch parameters, LDS tile movement helpers and block mapping.
+
+#include "tilemix_device.h"
+#include "tilemix_launch.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace tilemix {
+
+inline constexpr float kLog2e = 1.4426950408889634f;
+inline constexpr int kXcds = 8;                               // MI355X: 8 XCDs, workgroups dealt round-robin
+inline constexpr std::uint32_t kBufferFlags = 0x00020000u;    // raw buffer resource word 3, gfx9 family
+inline constexpr int kOutOfRange = static_cast<int>(0x80000000u);  // buffer offset that reads as zero
+inline constexpr int kTileKeys = 64;                          // key tile = one K quantization block
+
+// Online-softmax scores enter as x * c (log2 domain) against a reference
+// maximum m that is raised lazily - only when a tile's maximum exceeds it by
+// more than kLazyRescale (log2 units) - so most tiles skip the O rescale;
+// probabilities stay <= 2^kLazyRescale, far inside fp16 range. Every
+// probability and the running sum use the same m, so the common factor
+// cancels exactly in O = sum(p v) / sum(p).
+inline constexpr float kLazyRescale = 8.0f;
+
+struct AttnParams {
+    const std::uint16_t* Q;
+    const std::uint16_t* K;
+    const std::uint16_t* V;
+    float* O;
+    const std::int8_t* Q8;
+    const std::int8_t* K8;
+    const std::uint16_t* q_scales;
+    const std::uint16_t* k_scales;
+    const std::uint64_t* route_words;
+    const std::uint64_t* skip_words;
+    std::uint8_t* trace;
+    std::int32_t* dots;
+    std::int8_t* q8_out;
+    std::uint16_t* q_scales_out;
+    std::int64_t q_stride;
+    std::int64_t k_stride;
+    std::int64_t v_stride;
+    std::int64_t o_stride;
+    std::int64_t words_per_row;
+    std::int64_t words_per_head;
+    int heads;
+    int M;
+    int N;
+    int d;
+    int key_tiles_per_group;
+    int q_tiles16;
+    int key_tiles32;
+    int q_blocks;
+    int k_blocks;
+    int causal;
+    int fuse_q_quant;
+    int int8_operands;
+    float score_log2;  // score_scale * log2(e)
+    float score_scale;
+};
+
+__device__ __forceinline__ half8 concat(half4 a, half4 b) {
+    return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, element e of lane i comes
+// from lane 4e + i / 4, element i % 4 of that lane's 8-byte row piece.
+__device__ __forceinline__ half4 read_tr16(const unsigned char* lds_byte_address) {
+    const short4v raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(lds_byte_address));
+    return __builtin_bit_cast(half4, raw);
+}
+
+// 16 bytes per lane from buffer offset soffset + voffset into LDS at
+// lds_base + 16 * lane (lds_base is wave-uniform).
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds_base, int voffset,
+                                            int soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds_base), 16, voffset,
+                                             soffset, 0, 0);
+}
+
+// Offset of lane `lane`'s 16-byte piece of wave load `w` of a tile whose LDS
+// rows are `lds_stride` bytes apart: its row and 16-byte column follow from
+// where it lands (lds offset 1024 w + 16 lane). Padding slots and columns at
+// or beyond `row_bytes` (the valid bytes of a global row) read as zero.
+__device__ __forceinline__ int lane_offset(int w, int lane, int lds_stride, int row_bytes, int global_row_bytes) {
+    const int landing = 1024 * w + 16 * lane;
+    const int row = landing / lds_stride;
+    const int column = landing - row * lds_stride;
+    return column < row_bytes ? row * global_row_bytes + column : kOutOfRange;
+}
+
+// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt left unconstrained).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n <= 63, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier ordering LDS only: waits for this wave's LDS operations,
+// not for its vector-memory loads.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Workgroup index -> (head, row group). Workgroups are dealt round-robin to
+// the XCDs; all row groups of a head run on one XCD so that its K / V / K8
+// stay in that XCD's L2. Causal problems start the heaviest (last) row
+// groups first, head after head, to shorten the tail.
+__device__ __forceinline__ void map_block(int linear, int heads, int groups, bool causal, int& head, int& group) {
+    int slot_group;
+    if (heads % kXcds == 0) {
+        const int xcd = linear % kXcds, slot = linear / kXcds;
+        const int heads_per_xcd = heads / kXcds;
+        if (causal) {
+            head = xcd + kXcds * (slot % heads_per_xcd);
+            slot_group = slot / heads_per_xcd;
+        } else {
+            head = xcd + kXcds * (slot / groups);
+            slot_group = slot % groups;
+        }
+    } else if (causal) {
+        head = linear % heads;
+        slot_group = linear / heads;
+    } else {
+        head = linear / groups;
+        slot_group = linear % groups;
+    }
+    group = causal ? groups - 1 - slot_group : slot_group;
+}
+
+}  // namespace tilemix
