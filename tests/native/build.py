@@ -1,13 +1,17 @@
-"""Build the native test driver tests/native/_build/tilemix_test.
+"""Build the native test programs under tests/native/_build/.
 
-It restates src/tests/tilemix_test.cu against the HIP library's C++ API
-(include/attention_fused.h) and links the C oracle as its checker; build the
-library first (tilemix-cuda_amd/build.py).
+* tilemix_test restates src/tests/tilemix_test.cu against the HIP library's
+  C++ API (include/attention_fused.h) and links the C oracle as its checker;
+  build the library first (tilemix-cuda_amd/build.py).
+* quant_division_check runs the quantizer's division-free quotient against
+  IEEE division for every fp16 (block maximum, value) pair, compiled with the
+  library's own device flags.
 
 Usage: python tests/native/build.py
 """
 from __future__ import annotations
 
+import importlib.util
 import os
 import shutil
 import subprocess
@@ -17,6 +21,7 @@ HERE = Path(__file__).resolve().parent
 ROOT = HERE.parent.parent
 OUT = HERE / "_build"
 EXE = OUT / "tilemix_test"
+DIVISION_CHECK = OUT / "quant_division_check"
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
 
@@ -39,7 +44,20 @@ def build() -> Path:
           f"-L{ROOT / 'tilemix-cuda_amd'}", "-ltilemix_hip", "-Wl,-rpath,$ORIGIN/../../../tilemix-cuda_amd",
           "-o", str(tmp)])
     os.replace(tmp, EXE)
+    build_division_check()
     return EXE
+
+
+def build_division_check() -> Path:
+    spec = importlib.util.spec_from_file_location("tilemix_build", ROOT / "tilemix-cuda_amd" / "build.py")
+    library_build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(library_build)
+    OUT.mkdir(parents=True, exist_ok=True)
+    tmp = DIVISION_CHECK.with_suffix(".tmp")
+    _run([HIPCC, *[f for f in library_build.DEVICE_FLAGS if f != "-fPIC"], f"-I{ROOT / 'include'}",
+          f"-I{library_build.CSRC}", str(HERE / "quant_division_check.hip"), "-o", str(tmp)])
+    os.replace(tmp, DIVISION_CHECK)
+    return DIVISION_CHECK
 
 
 if __name__ == "__main__":

@@ -1,0 +1,69 @@
+// Exhaustive device check of the quantizer's division-free quotient
+// (tilemix_device.h: quotient / quantize_value_recip) against IEEE division
+// (quantize_value, built with -fhip-fp32-correctly-rounded-divide-sqrt):
+// for every positive finite fp16 block maximum a and every fp16 x with
+// |x| <= a, the fp32 quotients (as values) and the int8 results must agree.
+// Prints "PASS <pairs>" or the first mismatches; exit code 0 on pass.
+#include "tilemix_device.h"
+
+#include <cstdio>
+
+using namespace tilemix;
+
+__global__ void check(unsigned long long* pairs, unsigned long long* bad, unsigned* first) {
+    const unsigned a_bits = blockIdx.x + 1;  // 0x0001 .. 0x7bff: positive finite fp16
+    if (a_bits > 0x7bffu) return;
+    const float absmax = half_bits_to_float(static_cast<std::uint16_t>(a_bits));
+    const float scale = block_scale(absmax);
+    const float recip = 1.0f / scale;
+    unsigned long long n = 0, wrong = 0;
+    // x over all fp16 bit patterns with |x| <= absmax (magnitude bits <= a_bits), both signs.
+    for (unsigned m = threadIdx.x; m <= a_bits; m += blockDim.x) {
+        for (unsigned sign = 0; sign < 2; ++sign) {
+            const float x = half_bits_to_float(static_cast<std::uint16_t>(m | (sign << 15)));
+            const float exact = x / scale;
+            const float fast = quotient(x, scale, recip);
+            const int q_exact = quantize_value(x, scale);
+            const int q_fast = quantize_value_recip(x, scale, recip);
+            ++n;
+            // Quotients compare as floats: x = -0 gives -0 by division and +0 here,
+            // which quantize alike; every other quotient must match bit for bit.
+            if (exact != fast || q_exact != q_fast) {
+                ++wrong;
+                if (atomicCAS(first, 0u, (a_bits << 16) | m | (sign << 15)) == 0u) {}
+            }
+        }
+    }
+    atomicAdd(pairs, n);
+    if (wrong) atomicAdd(bad, wrong);
+}
+
+int main() {
+    unsigned long long *pairs, *bad;
+    unsigned* first;
+    if (hipMalloc(&pairs, 8) != hipSuccess || hipMalloc(&bad, 8) != hipSuccess || hipMalloc(&first, 4) != hipSuccess) {
+        std::puts("FAIL allocation");
+        return 2;
+    }
+    (void)hipMemset(pairs, 0, 8);
+    (void)hipMemset(bad, 0, 8);
+    (void)hipMemset(first, 0, 4);
+    check<<<0x7bff, 256>>>(pairs, bad, first);
+    unsigned long long n = 0, wrong = 0;
+    unsigned f = 0;
+    if (hipMemcpy(&n, pairs, 8, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(&wrong, bad, 8, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(&f, first, 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        std::puts("FAIL copy");
+        return 2;
+    }
+    (void)hipFree(pairs);
+    (void)hipFree(bad);
+    (void)hipFree(first);
+    if (wrong) {
+        std::printf("FAIL %llu of %llu pairs differ (first: absmax bits 0x%04x, x bits 0x%04x)\n", wrong, n, f >> 16, f & 0xffffu);
+        return 1;
+    }
+    std::printf("PASS %llu pairs\n", n);
+    return 0;
+}

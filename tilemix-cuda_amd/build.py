@@ -27,8 +27,9 @@ DEMO = BUILD / "tilemix_demo"
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-# Device flags: IEEE binary32 division for the bit-exact quantizer, and no
-# packed-FP32 VALU instructions (v_pk_*_f32) in generated code.
+# Device flags: correctly rounded binary32 division (the quantizer's
+# reciprocal 1/scale must be the IEEE one for its quotients to equal x/scale),
+# and no packed-FP32 VALU instructions (v_pk_*_f32) in generated code.
 DEVICE_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

@@ -211,6 +211,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             __syncthreads();
             absmax = fmaxf(fmaxf(group_max[0], group_max[1]), fmaxf(group_max[2], group_max[3]));
             const float scale = block_scale(absmax);
+            const float recip = 1.0f / scale;
             const _Float16 stored = static_cast<_Float16>(scale);
             q_scale = static_cast<float>(stored);
             if (tid == 0 && p.q_scales_out)
@@ -224,7 +225,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                     int v[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
-                        v[e] = dc < DC ? quantize_value(static_cast<float>(qf[b][dc < DC ? dc : 0][e]), scale) : 0;
+                        v[e] = dc < DC ? quantize_value_recip(static_cast<float>(qf[b][dc < DC ? dc : 0][e]), scale, recip) : 0;
                     uint2v packed;
                     packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
                     packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);

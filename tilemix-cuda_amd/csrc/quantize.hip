@@ -6,7 +6,10 @@
 // contiguous, a block is one contiguous span of rows*d halves: the vector path
 // reads it once with 16-byte loads into registers (at most 8 per thread),
 // reduces the absmax across the workgroup and quantizes from registers, so HBM
-// sees exactly one read of the input and one write of the int8 output.
+// sees exactly one read of the input and one write of the int8 output. The
+// absmax runs on packed fp16 pairs (magnitudes by clearing the sign bits) and
+// the per-element quotient uses the block's reciprocal with an exact
+// correction step instead of a division (quantize_value_recip).
 
 #include "tilemix_device.h"
 #include "tilemix_launch.h"
@@ -36,16 +39,22 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSid
     uint4v chunk[kQuantMaxChunks];
     const int chunks = count / 8;
     if constexpr (kVector) {
+        half8 magnitude{};  // elementwise maxima of |x| (fp16 max ignores NaN, as fmaxf does)
+        const uint4v sign_off{0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};
+        // Every lane issues all loads, past-the-end lanes from the block's last
+        // chunk (chunks >= 1 since d % 8 == 0), and keeps zeros instead; loads
+        // under a branch would serialise behind one wait each.
 #pragma unroll
         for (int c = 0; c < kQuantMaxChunks; ++c) {
             const int index = t + c * kQuantThreads;
-            if (index < chunks) {
-                chunk[c] = reinterpret_cast<const uint4v*>(in)[index];
-                const half8 h = __builtin_bit_cast(half8, chunk[c]);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) absmax = fmaxf(absmax, fabsf(static_cast<float>(h[e])));
-            }
+            const uint4v loaded = reinterpret_cast<const uint4v*>(in)[index < chunks ? index : chunks - 1];
+            chunk[c] = index < chunks ? loaded : uint4v{0u, 0u, 0u, 0u};
         }
+#pragma unroll
+        for (int c = 0; c < kQuantMaxChunks; ++c)
+            magnitude = __builtin_elementwise_max(magnitude, __builtin_bit_cast(half8, chunk[c] & sign_off));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) absmax = fmaxf(absmax, static_cast<float>(magnitude[e]));
     } else {
         for (int index = t; index < count; index += kQuantThreads)
             absmax = fmaxf(absmax, fabsf(half_bits_to_float(in[index])));
@@ -56,6 +65,7 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSid
     __syncthreads();
     absmax = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
     const float scale = block_scale(absmax);
+    const float recip = 1.0f / scale;  // used only when scale > 0
     if (t == 0) side.scales[head * side.blocks + block] = float_to_half_bits(scale);
 
     if constexpr (kVector) {
@@ -66,7 +76,7 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSid
                 const half8 h = __builtin_bit_cast(half8, chunk[c]);
                 int v[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = quantize_value(static_cast<float>(h[e]), scale);
+                for (int e = 0; e < 8; ++e) v[e] = quantize_value_recip(static_cast<float>(h[e]), scale, recip);
                 uint2v packed;
                 packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
                 packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);
@@ -75,7 +85,7 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSid
         }
     } else {
         for (int index = t; index < count; index += kQuantThreads)
-            out[index] = static_cast<std::int8_t>(quantize_value(half_bits_to_float(in[index]), scale));
+            out[index] = static_cast<std::int8_t>(quantize_value_recip(half_bits_to_float(in[index]), scale, recip));
     }
 }
 

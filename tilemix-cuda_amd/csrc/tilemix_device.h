@@ -49,6 +49,28 @@ __device__ __forceinline__ int quantize_value(float x, float scale) {
 // Block scale: fp32 absmax / 127 with IEEE rounding (src/tilemix.cu:37).
 __device__ __forceinline__ float block_scale(float absmax) { return absmax / 127.0f; }
 
+// x / scale rounded to nearest without a division per element (Markstein's
+// correction step): with recip = RN(1 / scale), y = RN(x * recip) is within
+// an ulp of the quotient, the fma gives its exact remainder, and one more fma
+// rounds to the correctly rounded quotient. The operands here are always
+// well scaled (|x| <= absmax = 127 * scale, scale a normal float or 0), and
+// the result equals IEEE x / scale for every fp16 x and fp16 absmax; the
+// exhaustive device check in tests/native/quant_division_check.hip pins that.
+__device__ __forceinline__ float quotient(float x, float scale, float recip) {
+    const float y = x * recip;
+    const float r = __builtin_fmaf(-scale, y, x);
+    return __builtin_fmaf(r, recip, y);
+}
+
+// quantize_value with the per-block reciprocal (recip = 1 / scale, any value
+// when scale == 0): the same bytes as quantize_value.
+__device__ __forceinline__ int quantize_value_recip(float x, float scale, float recip) {
+    const float normalized = scale > 0.0f ? quotient(x, scale, recip) : 0.0f;
+    const float shifted = normalized + __builtin_copysignf(0.5f, normalized);
+    const int rounded = static_cast<int>(shifted);
+    return rounded < -127 ? -127 : (rounded > 127 ? 127 : rounded);
+}
+
 __device__ __forceinline__ float wave_max(float value) {
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset));
