@@ -93,13 +93,13 @@ struct RowState {
 template <int kFB, bool kPrecise>
 __device__ __forceinline__ void softmax_tile(RowState<kFB>& st, int b, float4v (&x)[4], float c,
                                              half8 (&ph)[2], half8 (&pl)[2]) {
-    float tile = fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
-                       fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
-    tile = fmaxf(tile, fmaxf(fmaxf(fmaxf(x[2][0], x[2][1]), fmaxf(x[2][2], x[2][3])),
-                             fmaxf(fmaxf(x[3][0], x[3][1]), fmaxf(x[3][2], x[3][3]))));
+    const float t0 = max3(max3(x[0][0], x[0][1], x[0][2]), x[0][3], x[1][3]);
+    const float t1 = max3(x[1][0], x[1][1], x[1][2]);
+    const float t2 = max3(max3(x[2][0], x[2][1], x[2][2]), x[2][3], x[3][3]);
+    const float t3 = max3(x[3][0], x[3][1], x[3][2]);
+    float tile = max3(max3(t0, t1, t2), t3, t3);
     tile *= c;  // c >= 0 and rounding is monotone: max(x) * c == max(x * c)
-    tile = fmaxf(tile, __shfl_xor(tile, 16));
-    tile = fmaxf(tile, __shfl_xor(tile, 32));
+    tile = row_max4(tile);
     const bool raise = tile > st.m[b] + kLazyRescale;
     if (__any(raise)) {
         // Rows with no visible key yet keep m = -inf (their sums are still 0).
@@ -630,9 +630,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     // ---------------------------------------------------------- epilogue
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-        float l = st.l[b];
-        l += __shfl_xor(l, 16);  // the row's four lanes: i, i + 16, i + 32, i + 48
-        l += __shfl_xor(l, 32);
+        const float l = row_sum4(st.l[b]);  // the row's four lanes: i, i + 16, i + 32, i + 48
         const float inverse = l > 0.0f ? 1.0f / l : 0.0f;
         const int row = qw + 16 * b + i;
         if (row >= M) continue;
