@@ -289,7 +289,8 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         const int kt = 2 * j + (lane & 1);
         bool skip = true, int8 = false;
         if (my_row_valid && kt < p.key_tiles32) {
-            const std::int64_t group = kt / p.key_tiles_per_group;
+            const unsigned group = p.group_shift >= 0 ? static_cast<unsigned>(kt) >> p.group_shift
+                                                      : static_cast<unsigned>(kt) / static_cast<unsigned>(p.key_tiles_per_group);
             const std::int64_t block = group >> 6;
             if (block != cached_block) {
                 cached_block = block;
@@ -306,13 +307,9 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 
     // ------------------------------------------------------ tile movement
     const std::int64_t kv_bytes = static_cast<std::int64_t>(N) * d * 2;
-    __amdgpu_buffer_rsrc_t rsrc_k = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<std::uint16_t*>(Kh), 0, static_cast<int>(kv_bytes), kBufferFlags);
-    __amdgpu_buffer_rsrc_t rsrc_v = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<std::uint16_t*>(Vh), 0, static_cast<int>(kv_bytes), kBufferFlags);
-    __amdgpu_buffer_rsrc_t rsrc_k8 = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<std::int8_t*>(p.int8_operands ? K8h : p.K8), 0,
-        static_cast<int>(p.int8_operands ? kv_bytes / 2 : 0), kBufferFlags);
+    const int4v rsrc_k = make_rsrc(Kh, static_cast<int>(kv_bytes));
+    const int4v rsrc_v = make_rsrc(Vh, static_cast<int>(kv_bytes));
+    const int4v rsrc_k8 = make_rsrc(p.int8_operands ? K8h : p.K8, static_cast<int>(p.int8_operands ? kv_bytes / 2 : 0));
     int off_k[L::kKPerWave], off_v[L::kVPerWave], off_k8[L::kK8PerWave];
     if constexpr (kVector) {
 #pragma unroll
@@ -450,7 +447,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         if (active) {
             float k_factor = 0.0f;  // q_scale * k_scale * score_scale * log2(e)
             if (wave_int8) {
-                const float k_scale = half_bits_to_float(p.k_scales[head * p.k_blocks + j]);
+                const float k_scale = half_bits_to_float(load_uniform_u16(p.k_scales + head * p.k_blocks + j));
                 k_factor = ((q_scale * k_scale) * p.score_scale) * kLog2e;
             }
             // ---- scores S^T[kb][b]: lane (g, i) holds query i, keys 16kb + 4g + r
@@ -742,6 +739,7 @@ AttnParams base_params(const std::uint16_t* Q, const std::uint16_t* K, const std
     p.N = N;
     p.d = d;
     p.key_tiles_per_group = group;
+    p.group_shift = (group & (group - 1)) == 0 ? __builtin_ctz(static_cast<unsigned>(group)) : -1;
     p.q_tiles16 = (M - 1) / kCellRows + 1;
     p.key_tiles32 = (N - 1) / kCellKeys + 1;
     p.q_blocks = (M - 1) / kQBlockRows + 1;

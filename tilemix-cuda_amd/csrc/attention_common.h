@@ -51,6 +51,7 @@ struct AttnParams {
     int N;
     int d;
     int key_tiles_per_group;
+    int group_shift;  // log2(key_tiles_per_group) when that is a power of two, else -1
     int q_tiles16;
     int key_tiles32;
     int q_blocks;
@@ -111,12 +112,41 @@ __device__ __forceinline__ half4 read_tr16(const unsigned char* lds_byte_address
     return __builtin_bit_cast(half4, raw);
 }
 
+// Raw buffer resource (gfx9 layout) held in four SGPRs: base address,
+// stride 0, `bytes` records (offsets at or past it read as zero), flags.
+__device__ __forceinline__ int4v make_rsrc(const void* base, int bytes) {
+    const unsigned long long address = reinterpret_cast<unsigned long long>(base);
+    return int4v{__builtin_amdgcn_readfirstlane(static_cast<int>(address & 0xffffffffu)),
+                 __builtin_amdgcn_readfirstlane(static_cast<int>((address >> 32) & 0xffffu)),
+                 __builtin_amdgcn_readfirstlane(bytes), static_cast<int>(kBufferFlags)};
+}
+
 // 16 bytes per lane from buffer offset soffset + voffset into LDS at
-// lds_base + 16 * lane (lds_base is wave-uniform).
-__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds_base, int voffset,
-                                            int soffset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(lds_base), 16, voffset,
-                                             soffset, 0, 0);
+// lds_base + 16 * lane (lds_base is wave-uniform; M0 carries it). Issued as
+// inline assembly so that the compiler does not treat it as an LDS store: it
+// would otherwise wait for every outstanding tile load before any later LDS
+// read it cannot prove disjoint. The kernels order these loads themselves -
+// s_waitcnt vmcnt, then a workgroup barrier, before any read of the tile.
+__device__ __forceinline__ void load_to_lds(int4v rsrc, const unsigned char* lds_base, int voffset, int soffset) {
+    const unsigned lds_address = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(
+        reinterpret_cast<unsigned long long>((__attribute__((address_space(3))) const void*)(lds_base))));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_address), "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory");
+}
+
+// A 16-bit value at a wave-uniform address, read with s_load_dword (the
+// containing aligned dword) and waited on with lgkmcnt: a vector load here
+// would be waited on with vmcnt and so also wait for the tile loads above.
+__device__ __forceinline__ std::uint16_t load_uniform_u16(const std::uint16_t* address) {
+    const unsigned long long a = reinterpret_cast<unsigned long long>(address);
+    const unsigned lo = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a & ~3ull));
+    const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a >> 32));
+    const unsigned long long word_address = (static_cast<unsigned long long>(hi) << 32) | lo;
+    unsigned word;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(word) : "s"(word_address) : "memory");
+    return static_cast<std::uint16_t>((a & 2) ? (word >> 16) : (word & 0xffffu));
 }
 
 // Offset of lane `lane`'s 16-byte piece of wave load `w` of a tile whose LDS
