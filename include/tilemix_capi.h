@@ -139,6 +139,61 @@ int tilemix_quantize_qk_batched(const uint16_t* Q, const uint16_t* K, int8_t* Q8
                                 int N, int d, int64_t q_head_stride, int64_t k_head_stride,
                                 void* stream);
 
+/*
+ * Device-side routing-mask producer (no reference counterpart: the reference
+ * builds masks on the host, src/tests/tilemix_test.cu:432-448 and
+ * src/main.cu:48; this produces the same TileMixRouting word format,
+ * include/attention_fused.h:34-52, on the GPU).
+ *
+ * Tile codes are uint8 [heads][tiles_q][tiles_k] with tiles_q =
+ * ceil(M / tile_rows), tiles_k = ceil(N / tile_keys), values
+ * TILEMIX_ROUTE_FP16 / _INT8 / _SKIP; tiles must be whole 16-row x 32-key
+ * routing cells (tile_rows % 16 == 0, tile_keys % 32 == 0). Random builders
+ * draw u = (splitmix64(seed ^ splitmix64(2 * index + salt)) >> 40) / 2^24 for
+ * tile linear index (head * tiles_q + i) * tiles_k + j (salt 0), so the codes
+ * depend only on (seed, head, tile). Errors: null pointer, non-positive size,
+ * bad tile shape or probability outside [0, 1] -> InvalidValue.
+ */
+
+/* Packs tile codes into route_words and skip_words, each heads *
+ * tilemix_routing_word_count_c(M, N, key_tiles_per_group) words, contiguous
+ * per head: bit = INT8 (route) or skip (skip), other codes FP16. A key-tile
+ * group must not straddle two tiles: (tile_keys / 32) % key_tiles_per_group
+ * == 0, else InvalidValue. */
+int tilemix_routes_from_tiles(const uint8_t* tile_codes, int heads, int M, int N, int tile_rows,
+                              int tile_keys, int key_tiles_per_group, uint64_t* route_words,
+                              uint64_t* skip_words, void* stream);
+
+/* Each tile INT8 when u < p_int8, else FP16. */
+int tilemix_tiles_bernoulli(uint8_t* tile_codes, int heads, int M, int N, int tile_rows, int tile_keys,
+                            float p_int8, uint64_t seed, void* stream);
+
+/* Square causal problem (M = N = S): tile (i, j) is SKIP
+ * when j > last = (i * tile_rows + tile_rows - 1) / tile_keys, FP16 when
+ * last - j < fp16_band, otherwise INT8 when u < p_int8, else FP16. */
+int tilemix_tiles_causal_band(uint8_t* tile_codes, int heads, int S, int tile_rows, int tile_keys,
+                              int fp16_band, float p_int8, uint64_t seed, void* stream);
+
+/* SKIP when u < p_skip, INT8 when u < p_skip + p_int8, else FP16 (BASELINE
+ * config 5); a tile row left all SKIP gets tile j = splitmix64(seed ^
+ * splitmix64(2 * (head * tiles_q + i) + 1)) % tiles_k forced FP16.
+ * p_skip + p_int8 > 1 -> InvalidValue. */
+int tilemix_tiles_three_way(uint8_t* tile_codes, int heads, int M, int N, int tile_rows, int tile_keys,
+                            float p_skip, float p_int8, uint64_t seed, void* stream);
+
+/* Importance router: per head, the round-half-even(
+ * fp16_fraction * tiles_q * tiles_k) tiles with the largest bound
+ * d * amax|Q tile rows| * amax|K tile keys| are FP16 (ties to the lower
+ * linear tile index), the rest INT8. Head h of Q/K starts at h *
+ * {q,k}_head_stride elements (ignored when heads == 1). `workspace` is device
+ * scratch of at least tilemix_importance_workspace_bytes(...) bytes (the
+ * per-tile maxima); tiles_q + tiles_k > 16384 -> NotSupported. */
+size_t tilemix_importance_workspace_bytes(int heads, int M, int N, int tile_rows, int tile_keys);
+int tilemix_tiles_importance(const uint16_t* Q, const uint16_t* K, int heads, int M, int N, int d,
+                             int64_t q_head_stride, int64_t k_head_stride, int tile_rows, int tile_keys,
+                             float fp16_fraction, float* workspace, size_t workspace_bytes,
+                             uint8_t* tile_codes, void* stream);
+
 /* FFI mirrors of the constexpr sizing helpers of attention_fused.h:21-45, for
  * callers that cannot evaluate C++ constexpr functions. */
 size_t tilemix_routing_words_per_row_c(int N, int key_tiles_per_group);

@@ -146,6 +146,41 @@ def test_batched_validation_codes(tm):
     assert run(score_dots=w) == INVALID                        # dots need INT8 routes
 
 
+def test_mask_producer_validation_codes(tm):
+    """The device mask producer rejects bad arguments before any HIP call."""
+    fake = 0x1000  # never dereferenced: every case below fails validation first
+    # packer: null pointers, sizes, tile shapes, a key-tile group straddling two tiles
+    assert tm.routes_from_tiles(None, 1, 64, 64, 64, 64, 2, fake, fake) == INVALID
+    assert tm.routes_from_tiles(fake, 1, 64, 64, 64, 64, 2, None, fake) == INVALID
+    assert tm.routes_from_tiles(fake, 1, 64, 64, 64, 64, 2, fake, None) == INVALID
+    assert tm.routes_from_tiles(fake, 0, 64, 64, 64, 64, 2, fake, fake) == INVALID
+    assert tm.routes_from_tiles(fake, 1, 0, 64, 64, 64, 2, fake, fake) == INVALID
+    assert tm.routes_from_tiles(fake, 1, 64, 64, 24, 64, 2, fake, fake) == INVALID   # not whole 16-row cells
+    assert tm.routes_from_tiles(fake, 1, 64, 64, 64, 48, 1, fake, fake) == INVALID   # not whole 32-key cells
+    assert tm.routes_from_tiles(fake, 1, 64, 64, 64, 32, 2, fake, fake) == INVALID   # group of 2 spans 2 tiles
+    assert tm.routes_from_tiles(fake, 1, 64, 64, 64, 96, 2, fake, fake) == INVALID   # 3 cells per tile, g = 2
+    assert tm.routes_from_tiles(fake, 1, 64, 64, 64, 64, 0, fake, fake) == INVALID
+    # builders: probabilities, band, shapes
+    assert tm.tiles_bernoulli(fake, 1, 64, 64, 64, 64, 1.5, 0) == INVALID
+    assert tm.tiles_bernoulli(fake, 1, 64, 64, 64, 64, float("nan"), 0) == INVALID
+    assert tm.tiles_bernoulli(None, 1, 64, 64, 64, 64, 0.5, 0) == INVALID
+    assert tm.tiles_causal_band(fake, 1, 64, 128, 64, -1, 0.5, 0) == INVALID
+    assert tm.tiles_causal_band(fake, 1, 0, 128, 64, 8, 0.5, 0) == INVALID
+    assert tm.tiles_three_way(fake, 1, 64, 64, 64, 64, 0.7, 0.4, 0) == INVALID   # p_skip + p_int8 > 1
+    assert tm.tiles_three_way(fake, 1, 64, 64, 64, 64, -0.1, 0.4, 0) == INVALID
+    # importance router: workspace sizing and checks
+    assert tm.importance_workspace_bytes(32, 16384, 16384, 128, 64) == 32 * (128 + 256) * 4
+    assert tm.importance_workspace_bytes(0, 16384, 16384, 128, 64) == 0
+    need = tm.importance_workspace_bytes(2, 256, 256, 128, 64)
+    assert tm.tiles_importance(fake, fake, 2, 256, 256, 64, 128, 64, 0.25, fake, need - 1, fake) == INVALID
+    assert tm.tiles_importance(fake, fake, 2, 256, 256, 64, 128, 64, 1.25, fake, need, fake) == INVALID
+    assert tm.tiles_importance(None, fake, 2, 256, 256, 64, 128, 64, 0.25, fake, need, fake) == INVALID
+    assert tm.tiles_importance(fake, fake, 2, 256, 256, 64, 128, 64, 0.25, fake, need, fake,
+                               q_head_stride=100) == INVALID                        # overlapping heads
+    huge = tm.importance_workspace_bytes(1, 16 * 20000, 64, 16, 64)
+    assert tm.tiles_importance(fake, fake, 1, 16 * 20000, 64, 64, 16, 64, 0.25, fake, huge, fake) == NOT_SUPPORTED
+
+
 def test_missing_library_fails_loudly(tmp_path):
     code = ("import sys; sys.path.insert(0, %r)\n"
             "import tilemix\n"

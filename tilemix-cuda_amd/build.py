@@ -44,7 +44,7 @@ DEVICE_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-LIB_SOURCES = ["quantize.hip", "attention.hip"]
+LIB_SOURCES = ["quantize.hip", "attention.hip", "routing.hip"]
 SOURCE_FLAGS: dict[str, list[str]] = {}
 
 

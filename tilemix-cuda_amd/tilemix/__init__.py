@@ -23,6 +23,12 @@ from .api import (  # noqa: F401
     library_path,
     quantize_tilemix_qk,
     quantize_tilemix_qk_batched,
+    importance_workspace_bytes,
+    routes_from_tiles,
+    tiles_bernoulli,
+    tiles_causal_band,
+    tiles_importance,
+    tiles_three_way,
     routing_word_count,
     routing_words_per_row,
     shared_bytes,

@@ -78,6 +78,20 @@ def library() -> ctypes.CDLL:
         so.tilemix_shared_bytes_c.restype = sz
         so.tilemix_version.argtypes = []
         so.tilemix_version.restype = ctypes.c_char_p
+        u64 = ctypes.c_uint64
+        so.tilemix_routes_from_tiles.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp]
+        so.tilemix_routes_from_tiles.restype = i32
+        so.tilemix_tiles_bernoulli.argtypes = [vp, i32, i32, i32, i32, i32, f32, u64, vp]
+        so.tilemix_tiles_bernoulli.restype = i32
+        so.tilemix_tiles_causal_band.argtypes = [vp, i32, i32, i32, i32, i32, f32, u64, vp]
+        so.tilemix_tiles_causal_band.restype = i32
+        so.tilemix_tiles_three_way.argtypes = [vp, i32, i32, i32, i32, i32, f32, f32, u64, vp]
+        so.tilemix_tiles_three_way.restype = i32
+        so.tilemix_importance_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
+        so.tilemix_importance_workspace_bytes.restype = sz
+        so.tilemix_tiles_importance.argtypes = [vp, vp, i32, i32, i32, i32, i64, i64, i32, i32, f32, vp, sz,
+                                                vp, vp]
+        so.tilemix_tiles_importance.restype = i32
         _lib = so
     return _lib
 
@@ -208,3 +222,49 @@ def quantize_tilemix_qk_batched(Q, K, Q8, K8, q_scales, k_scales, heads: int, M:
     return library().tilemix_quantize_qk_batched(
         _ptr(Q), _ptr(K), _ptr(Q8), _ptr(K8), _ptr(q_scales), _ptr(k_scales), heads, M, N, d,
         q_head_stride or M * d, k_head_stride or N * d, _stream(stream))
+
+
+# ------------------------------------------------------- device mask producer
+# Extensions with no reference counterpart (the reference builds masks on
+# the host, src/tests/tilemix_test.cu:432-448): tile codes [heads, tiles_q,
+# tiles_k] uint8 (0 FP16, 1 INT8, 2 skip) built on the GPU, then packed into
+# the TileMixRouting word format (include/attention_fused.h:34-52).
+
+
+def routes_from_tiles(tile_codes, heads: int, M: int, N: int, tile_rows: int, tile_keys: int,
+                      key_tiles_per_group: int, route_words, skip_words, stream=None) -> int:
+    return library().tilemix_routes_from_tiles(_ptr(tile_codes), heads, M, N, tile_rows, tile_keys,
+                                               key_tiles_per_group, _ptr(route_words), _ptr(skip_words),
+                                               _stream(stream))
+
+
+def tiles_bernoulli(tile_codes, heads: int, M: int, N: int, tile_rows: int, tile_keys: int, p_int8: float,
+                    seed: int, stream=None) -> int:
+    return library().tilemix_tiles_bernoulli(_ptr(tile_codes), heads, M, N, tile_rows, tile_keys, p_int8,
+                                             seed, _stream(stream))
+
+
+def tiles_causal_band(tile_codes, heads: int, S: int, tile_rows: int, tile_keys: int, fp16_band: int,
+                      p_int8: float, seed: int, stream=None) -> int:
+    return library().tilemix_tiles_causal_band(_ptr(tile_codes), heads, S, tile_rows, tile_keys, fp16_band,
+                                               p_int8, seed, _stream(stream))
+
+
+def tiles_three_way(tile_codes, heads: int, M: int, N: int, tile_rows: int, tile_keys: int, p_skip: float,
+                    p_int8: float, seed: int, stream=None) -> int:
+    return library().tilemix_tiles_three_way(_ptr(tile_codes), heads, M, N, tile_rows, tile_keys, p_skip,
+                                             p_int8, seed, _stream(stream))
+
+
+def importance_workspace_bytes(heads: int, M: int, N: int, tile_rows: int, tile_keys: int) -> int:
+    return library().tilemix_importance_workspace_bytes(heads, M, N, tile_rows, tile_keys)
+
+
+def tiles_importance(Q, K, heads: int, M: int, N: int, d: int, tile_rows: int, tile_keys: int,
+                     fp16_fraction: float, workspace, workspace_bytes: int, tile_codes,
+                     q_head_stride: int = 0, k_head_stride: int = 0, stream=None) -> int:
+    return library().tilemix_tiles_importance(_ptr(Q), _ptr(K), heads, M, N, d, q_head_stride or M * d,
+                                              k_head_stride or N * d, tile_rows, tile_keys, fp16_fraction,
+                                              _ptr(workspace), workspace_bytes, _ptr(tile_codes),
+                                              _stream(stream))
+
