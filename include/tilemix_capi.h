@@ -65,6 +65,11 @@ int tilemix_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* V, f
                       const int8_t* Q8, const int8_t* K8, const uint16_t* q_scales,
                       const uint16_t* k_scales, int32_t* score_dots);
 
+/* Element types of O for the batched entry point (o_dtype). */
+#define TILEMIX_DTYPE_F32 0
+#define TILEMIX_DTYPE_F16 1
+#define TILEMIX_DTYPE_BF16 2
+
 /* Routing codes written to decoded_bits by the batched entry point. */
 #define TILEMIX_ROUTE_FP16 0
 #define TILEMIX_ROUTE_INT8 1
@@ -98,6 +103,16 @@ int tilemix_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* V, f
  * Per-head sizes: route/skip words tilemix_routing_word_count(M, N, g);
  * decoded_bits ceil(M/16)*ceil(N/32) bytes; score_dots M*N; Q8 M*d; K8 N*d;
  * q_scales ceil(M/128); k_scales ceil(N/64) - all contiguous per head.
+ *
+ * Layout and output options (appended; zero keeps the behaviour above):
+ *   o_dtype       TILEMIX_DTYPE_F32 (O is float), _F16 or _BF16 (O holds
+ *                 16-bit values rounded to nearest even from the same fp32
+ *                 result); o_head_stride then counts 16-bit elements;
+ *   *_row_stride  elements between consecutive rows of one head (0 = d), so
+ *                 e.g. a [B, S, H, D] tensor is head stride D, row stride
+ *                 H * D. Heads must not overlap: either each head ends
+ *                 before the next begins, or all heads interleave inside
+ *                 every row. Q8/K8 stay contiguous [rows][d] per head.
  */
 typedef struct TileMixBatchedArgs {
     const uint16_t* Q;
@@ -125,6 +140,11 @@ typedef struct TileMixBatchedArgs {
     uint16_t* q_scales;
     uint16_t* k_scales;
     int32_t* score_dots;
+    int o_dtype;
+    int64_t q_row_stride;
+    int64_t k_row_stride;
+    int64_t v_row_stride;
+    int64_t o_row_stride;
 } TileMixBatchedArgs;
 
 /* Multi-head attention (extension, see TileMixBatchedArgs). */
@@ -193,6 +213,15 @@ int tilemix_tiles_importance(const uint16_t* Q, const uint16_t* K, int heads, in
                              int64_t q_head_stride, int64_t k_head_stride, int tile_rows, int tile_keys,
                              float fp16_fraction, float* workspace, size_t workspace_bytes,
                              uint8_t* tile_codes, void* stream);
+
+/* tilemix_quantize_qk_batched with row strides (elements between consecutive
+ * rows of a head, 0 = d) for row-strided Q/K such as [B, S, H, D] tensors;
+ * the outputs stay contiguous per head. Head/row strides must not make heads
+ * overlap (see TileMixBatchedArgs). */
+int tilemix_quantize_qk_strided(const uint16_t* Q, const uint16_t* K, int8_t* Q8, int8_t* K8,
+                                uint16_t* q_scales, uint16_t* k_scales, int heads, int M, int N,
+                                int d, int64_t q_head_stride, int64_t k_head_stride,
+                                int64_t q_row_stride, int64_t k_row_stride, void* stream);
 
 /* FFI mirrors of the constexpr sizing helpers of attention_fused.h:21-45, for
  * callers that cannot evaluate C++ constexpr functions. */

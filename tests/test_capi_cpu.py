@@ -144,6 +144,20 @@ def test_batched_validation_codes(tm):
     assert run(route_words=w, K8=b, k_scales=s) == INVALID     # quantize=0 needs Q8 and q_scales
     assert run(route_words=w, K8=b, k_scales=s, quantize=2, Q8=b) == INVALID  # Q8 without q_scales
     assert run(score_dots=w) == INVALID                        # dots need INT8 routes
+    # layout and output options
+    assert run(o_dtype=3) == INVALID
+    assert run(o_dtype=-1) == INVALID
+    assert run(d=4, q_row_stride=3) == INVALID                 # rows closer than d
+    assert run(d=4, o_row_stride=2) == INVALID
+    # heads interleaved in rows too short to hold them all overlap
+    assert run(heads=2, M=4, N=4, d=4, q_head_stride=4, k_head_stride=4, v_head_stride=4, o_head_stride=4,
+               q_row_stride=8, k_row_stride=8, v_row_stride=8, o_row_stride=6) == INVALID
+    assert run(heads=3, M=4, N=4, d=4, q_head_stride=4, k_head_stride=4, v_head_stride=4, o_head_stride=4,
+               q_row_stride=8, k_row_stride=8, v_row_stride=8, o_row_stride=8) == INVALID
+    strided = tm.quantize_tilemix_qk_strided
+    assert strided(x, x, b, b, s, s, 1, 4, 4, 4, q_row_stride=2) == INVALID
+    assert strided(x, x, b, b, s, s, 2, 4, 4, 4, q_head_stride=4, k_head_stride=16, q_row_stride=6) == INVALID
+    assert strided(x, x, b, b, s, s, 1, 4, 4, 129) == NOT_SUPPORTED
 
 
 def test_mask_producer_validation_codes(tm):

@@ -171,7 +171,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     const std::uint16_t* Kh = p.K + head * p.k_stride;
     const std::uint16_t* Vh = p.V + head * p.v_stride;
     const std::int8_t* K8h = p.K8 + head * static_cast<std::int64_t>(N) * d;
-    float* Oh = p.O + head * p.o_stride;
+    unsigned char* const Oh = static_cast<unsigned char*>(p.O) + head * p.o_stride * (p.o_dtype == TILEMIX_DTYPE_F32 ? 4 : 2);
 
     // ---------------------------------------------------------------- Q
     half8 qf[2][DC];
@@ -183,13 +183,13 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             const int feature = 32 * dc + 8 * g;
             if constexpr (kVector) {
                 qf[b][dc] = (row < M && feature < d)
-                    ? *reinterpret_cast<const half8*>(Qh + static_cast<std::int64_t>(row) * d + feature)
+                    ? *reinterpret_cast<const half8*>(Qh + static_cast<std::int64_t>(row) * p.q_row + feature)
                     : half8{};
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
                     qf[b][dc][e] = (row < M && feature + e < d)
-                        ? __builtin_bit_cast(_Float16, Qh[static_cast<std::int64_t>(row) * d + feature + e])
+                        ? __builtin_bit_cast(_Float16, Qh[static_cast<std::int64_t>(row) * p.q_row + feature + e])
                         : static_cast<_Float16>(0.0f);
             }
         }
@@ -306,18 +306,22 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     };
 
     // ------------------------------------------------------ tile movement
-    const std::int64_t kv_bytes = static_cast<std::int64_t>(N) * d * 2;
-    const int4v rsrc_k = make_rsrc(Kh, static_cast<int>(kv_bytes));
-    const int4v rsrc_v = make_rsrc(Vh, static_cast<int>(kv_bytes));
-    const int4v rsrc_k8 = make_rsrc(p.int8_operands ? K8h : p.K8, static_cast<int>(p.int8_operands ? kv_bytes / 2 : 0));
+    // Buffer ranges end after the last row's d elements; row strides apart.
+    const std::int64_t k_bytes = (static_cast<std::int64_t>(N - 1) * p.k_row + d) * 2;
+    const std::int64_t v_bytes = (static_cast<std::int64_t>(N - 1) * p.v_row + d) * 2;
+    const int4v rsrc_k = make_rsrc(Kh, static_cast<int>(k_bytes));
+    const int4v rsrc_v = make_rsrc(Vh, static_cast<int>(v_bytes));
+    const int4v rsrc_k8 = make_rsrc(p.int8_operands ? K8h : p.K8,
+                                    static_cast<int>(p.int8_operands ? static_cast<std::int64_t>(N) * d : 0));
+    const int k_row_bytes = static_cast<int>(p.k_row * 2), v_row_bytes = static_cast<int>(p.v_row * 2);
     int off_k[L::kKPerWave], off_v[L::kVPerWave], off_k8[L::kK8PerWave];
     if constexpr (kVector) {
 #pragma unroll
         for (int t = 0; t < L::kKPerWave; ++t)
-            off_k[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kKStride, 2 * d, 2 * d);
+            off_k[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kKStride, 2 * d, k_row_bytes);
 #pragma unroll
         for (int t = 0; t < L::kVPerWave; ++t)
-            off_v[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kVStride, 2 * d, 2 * d);
+            off_v[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kVStride, 2 * d, v_row_bytes);
 #pragma unroll
         for (int t = 0; t < L::kK8PerWave; ++t)
             off_k8[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kK8Stride, d, d);
@@ -330,7 +334,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 #pragma unroll
                 for (int t = 0; t < L::kKPerWave; ++t) {
                     const int w = wave + kWavesPerGroup * t;
-                    if (w < L::kKLoads) load_to_lds(rsrc_k, lds_k + 1024 * w, off_k[t], k0 * d * 2);
+                    if (w < L::kKLoads) load_to_lds(rsrc_k, lds_k + 1024 * w, off_k[t], k0 * k_row_bytes);
                 }
             }
             if (need8) {
@@ -345,7 +349,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
                     const int row = e / kDP, f = e % kDP, key = k0 + row;
                     *reinterpret_cast<std::uint16_t*>(lds_k + row * L::kKStride + 2 * f) =
-                        (key < N && f < d) ? Kh[static_cast<std::int64_t>(key) * d + f] : 0;
+                        (key < N && f < d) ? Kh[static_cast<std::int64_t>(key) * p.k_row + f] : 0;
                 }
             }
             if (need8) {
@@ -363,13 +367,13 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 #pragma unroll
             for (int t = 0; t < L::kVPerWave; ++t) {
                 const int w = wave + kWavesPerGroup * t;
-                if (w < L::kVLoads) load_to_lds(rsrc_v, lds_v + 1024 * w, off_v[t], k0 * d * 2);
+                if (w < L::kVLoads) load_to_lds(rsrc_v, lds_v + 1024 * w, off_v[t], k0 * v_row_bytes);
             }
         } else {
             for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
                 const int row = e / kDP, f = e % kDP, key = k0 + row;
                 *reinterpret_cast<std::uint16_t*>(lds_v + row * L::kVStride + 2 * f) =
-                    (key < N && f < d) ? Vh[static_cast<std::int64_t>(key) * d + f] : 0;
+                    (key < N && f < d) ? Vh[static_cast<std::int64_t>(key) * p.v_row + f] : 0;
             }
         }
     };
@@ -631,18 +635,11 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         const float inverse = l > 0.0f ? 1.0f / l : 0.0f;
         const int row = qw + 16 * b + i;
         if (row >= M) continue;
-        float* out_row = Oh + static_cast<std::int64_t>(row) * d;
+        const std::int64_t row_offset = static_cast<std::int64_t>(row) * p.o_row;
 #pragma unroll
         for (int fb = 0; fb < kFB; ++fb) {
             const int feature = 16 * fb + 4 * g;
-            const float4v value = st.o[b][fb] * inverse;
-            if constexpr (kVector) {
-                if (feature < d) *reinterpret_cast<float4v*>(out_row + feature) = value;
-            } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (feature + r < d) out_row[feature + r] = value[r];
-            }
+            store_output(Oh, p.o_dtype, row_offset + feature, st.o[b][fb] * inverse, d - feature, kVector);
         }
     }
 }
@@ -709,10 +706,13 @@ hipError_t launch_attention(const AttnParams& p, bool precise, hipStream_t strea
     if (status != hipSuccess) return status;
     // The vector path moves 16-byte pieces and addresses a head's K / V with
     // 32-bit buffer offsets; other shapes take the element-wise path.
+    const std::int64_t k_range = (static_cast<std::int64_t>(p.N - 1) * p.k_row + p.d) * 2;
+    const std::int64_t v_range = (static_cast<std::int64_t>(p.N - 1) * p.v_row + p.d) * 2;
     bool vector = p.d % 16 == 0 && aligned(p.Q, 16) && aligned(p.K, 16) && aligned(p.V, 16) &&
                   aligned(p.O, 16) && p.q_stride % 8 == 0 && p.k_stride % 8 == 0 &&
-                  p.v_stride % 8 == 0 && p.o_stride % 4 == 0 &&
-                  static_cast<std::int64_t>(p.N) * p.d * 2 < (std::int64_t{1} << 31);
+                  p.v_stride % 8 == 0 && p.o_stride % 4 == 0 && p.q_row % 8 == 0 &&
+                  p.k_row % 8 == 0 && p.v_row % 8 == 0 && p.o_row % 4 == 0 &&
+                  k_range < (std::int64_t{1} << 31) && v_range < (std::int64_t{1} << 31);
     if (p.int8_operands) {
         if (!p.fuse_q_quant) vector = vector && aligned(p.Q8, 16);
         if (p.q8_out) vector = vector && aligned(p.q8_out, 8);
@@ -752,6 +752,8 @@ AttnParams base_params(const std::uint16_t* Q, const std::uint16_t* K, const std
     p.k_stride = static_cast<std::int64_t>(N) * d;
     p.v_stride = static_cast<std::int64_t>(N) * d;
     p.o_stride = static_cast<std::int64_t>(M) * d;
+    p.q_row = p.k_row = p.v_row = p.o_row = d;
+    p.o_dtype = TILEMIX_DTYPE_F32;
     return p;
 }
 
@@ -800,12 +802,16 @@ extern "C" int tilemix_attention_batched(const TileMixBatchedArgs* args, void* s
         !std::isfinite(a.score_scale) || group <= 0)
         return hipErrorInvalidValue;
     if (a.d > kMaxHeadDim) return hipErrorNotSupported;
-    if (a.heads > 1) {
-        const std::int64_t qn = static_cast<std::int64_t>(a.M) * a.d;
-        const std::int64_t kn = static_cast<std::int64_t>(a.N) * a.d;
-        if (a.q_head_stride < qn || a.o_head_stride < qn || a.k_head_stride < kn || a.v_head_stride < kn)
-            return hipErrorInvalidValue;
-    }
+    if (a.o_dtype < TILEMIX_DTYPE_F32 || a.o_dtype > TILEMIX_DTYPE_BF16) return hipErrorInvalidValue;
+    const std::int64_t q_row = a.q_row_stride ? a.q_row_stride : a.d;
+    const std::int64_t k_row = a.k_row_stride ? a.k_row_stride : a.d;
+    const std::int64_t v_row = a.v_row_stride ? a.v_row_stride : a.d;
+    const std::int64_t o_row = a.o_row_stride ? a.o_row_stride : a.d;
+    if (!strided_heads_ok(a.heads, a.M, a.d, a.q_head_stride, q_row) ||
+        !strided_heads_ok(a.heads, a.M, a.d, a.o_head_stride, o_row) ||
+        !strided_heads_ok(a.heads, a.N, a.d, a.k_head_stride, k_row) ||
+        !strided_heads_ok(a.heads, a.N, a.d, a.v_head_stride, v_row))
+        return hipErrorInvalidValue;
     const bool int8 = a.route_words != nullptr;
     if (a.quantize < 0 || a.quantize > 2) return hipErrorInvalidValue;
     if (int8) {
@@ -816,8 +822,8 @@ extern "C" int tilemix_attention_batched(const TileMixBatchedArgs* args, void* s
         return hipErrorInvalidValue;
     }
     if (a.quantize == 1 && int8) {
-        const QuantSide none = make_quant_side(nullptr, nullptr, nullptr, 0, 1, kQBlockRows);
-        const QuantSide k = make_quant_side(a.K, a.K8, a.k_scales, a.k_head_stride, a.N, kKBlockRows);
+        const QuantSide none = make_quant_side(nullptr, nullptr, nullptr, 0, 1, kQBlockRows, a.d);
+        const QuantSide k = make_quant_side(a.K, a.K8, a.k_scales, a.k_head_stride, a.N, kKBlockRows, k_row);
         const hipError_t status = check_device();
         if (status != hipSuccess) return status;
         const hipError_t quant = launch_quantize(none, k, a.heads, a.d, static_cast<hipStream_t>(stream));
@@ -834,6 +840,11 @@ extern "C" int tilemix_attention_batched(const TileMixBatchedArgs* args, void* s
         p.k_stride = static_cast<std::int64_t>(a.N) * a.d;
         p.v_stride = p.k_stride;
     }
+    p.q_row = q_row;
+    p.k_row = k_row;
+    p.v_row = v_row;
+    p.o_row = o_row;
+    p.o_dtype = a.o_dtype;
     p.causal = a.causal != 0;
     p.route_words = a.route_words;
     p.skip_words = a.skip_words;

@@ -2,6 +2,7 @@
 // Definitions of the attention kernel (attention.hip) kept apart from it:
 // launch parameters, LDS tile movement helpers and block mapping.
 
+#include "tilemix_capi.h"
 #include "tilemix_device.h"
 #include "tilemix_launch.h"
 
@@ -29,7 +30,7 @@ struct AttnParams {
     const std::uint16_t* Q;
     const std::uint16_t* K;
     const std::uint16_t* V;
-    float* O;
+    void* O;  // element type by o_dtype
     const std::int8_t* Q8;
     const std::int8_t* K8;
     const std::uint16_t* q_scales;
@@ -44,6 +45,11 @@ struct AttnParams {
     std::int64_t k_stride;
     std::int64_t v_stride;
     std::int64_t o_stride;
+    // Elements between consecutive rows of one head (>= d; d = dense rows).
+    std::int64_t q_row;
+    std::int64_t k_row;
+    std::int64_t v_row;
+    std::int64_t o_row;
     std::int64_t words_per_row;
     std::int64_t words_per_head;
     int heads;
@@ -59,6 +65,7 @@ struct AttnParams {
     int causal;
     int fuse_q_quant;
     int int8_operands;
+    int o_dtype;  // TILEMIX_DTYPE_F32 / _F16 / _BF16
     float score_log2;  // score_scale * log2(e)
     float score_scale;
 };
@@ -136,6 +143,42 @@ __device__ __forceinline__ void load_to_lds(int4v rsrc, const unsigned char* lds
                  : "memory");
 }
 
+// bf16 bits of x, rounded to nearest even (NaN stays a quiet NaN).
+__device__ __forceinline__ std::uint16_t float_to_bf16_bits(float x) {
+    const std::uint32_t u = __builtin_bit_cast(std::uint32_t, x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<std::uint16_t>((u >> 16) | 0x40u);
+    return static_cast<std::uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Stores four consecutive outputs of one row at element `offset` of `base`
+// in the output type (fp32, or fp16 / bf16 rounded to nearest even); only
+// the first `valid` (may be <= 0) are written. `vector`: the row is 16-byte
+// aligned and valid >= 4 whenever valid > 0.
+__device__ __forceinline__ void store_output(unsigned char* base, int dtype, std::int64_t offset, float4v value,
+                                             int valid, bool vector) {
+    if (valid <= 0) return;
+    if (dtype == TILEMIX_DTYPE_F32) {
+        float* out = reinterpret_cast<float*>(base) + offset;
+        if (vector) {
+            *reinterpret_cast<float4v*>(out) = value;
+        } else {
+            for (int r = 0; r < 4 && r < valid; ++r) out[r] = value[r];
+        }
+        return;
+    }
+    std::uint16_t bits[4];
+    for (int r = 0; r < 4; ++r)
+        bits[r] = dtype == TILEMIX_DTYPE_F16 ? __builtin_bit_cast(std::uint16_t, static_cast<_Float16>(value[r]))
+                                             : float_to_bf16_bits(value[r]);
+    std::uint16_t* out = reinterpret_cast<std::uint16_t*>(base) + offset;
+    if (vector) {
+        *reinterpret_cast<uint2v*>(out) = uint2v{bits[0] | (static_cast<std::uint32_t>(bits[1]) << 16),
+                                                 bits[2] | (static_cast<std::uint32_t>(bits[3]) << 16)};
+    } else {
+        for (int r = 0; r < 4 && r < valid; ++r) out[r] = bits[r];
+    }
+}
+
 // A 16-bit value at a wave-uniform address, read with s_load_dword (the
 // containing aligned dword) and waited on with lgkmcnt: a vector load here
 // would be waited on with vmcnt and so also wait for the tile loads above.
@@ -145,7 +188,8 @@ __device__ __forceinline__ std::uint16_t load_uniform_u16(const std::uint16_t* a
     const unsigned hi = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a >> 32));
     const unsigned long long word_address = (static_cast<unsigned long long>(hi) << 32) | lo;
     unsigned word;
-    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(word) : "s"(word_address) : "memory");
+    // Early clobber: the destination must not share registers with the address.
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=&s"(word) : "s"(word_address) : "memory");
     return static_cast<std::uint16_t>((a & 2) ? (word >> 16) : (word & 0xffffu));
 }
 

@@ -20,7 +20,10 @@ namespace {
 constexpr int kQuantThreads = 256;
 constexpr int kQuantMaxChunks = (128 * 128 / 8) / kQuantThreads;  // 16-byte chunks per thread
 
-template <bool kVector>
+// kContiguous: rows are d elements apart, so a block is one span of
+// rows * d halves; otherwise chunk c of the block is chunk c % (d / 8) of row
+// c / (d / 8).
+template <bool kVector, bool kContiguous>
 __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSide q, QuantSide k, int d) {
     __shared__ float partial[kQuantThreads / kWave];
     const bool is_q = static_cast<int>(blockIdx.x) < q.blocks;
@@ -30,7 +33,8 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSid
     const int first = block * side.block_rows;
     const int last = min(side.rows, first + side.block_rows);
     const int count = (last - first) * d;
-    const std::uint16_t* in = side.x + head * side.in_head_stride + static_cast<std::int64_t>(first) * d;
+    const std::uint16_t* in = side.x + head * side.in_head_stride + static_cast<std::int64_t>(first) * side.in_row_stride;
+    const std::int64_t row_stride = side.in_row_stride;
     std::int8_t* out = side.x8 + head * static_cast<std::int64_t>(side.rows) * d +
                        static_cast<std::int64_t>(first) * d;
     const int t = threadIdx.x;
@@ -47,7 +51,15 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSid
 #pragma unroll
         for (int c = 0; c < kQuantMaxChunks; ++c) {
             const int index = t + c * kQuantThreads;
-            const uint4v loaded = reinterpret_cast<const uint4v*>(in)[index < chunks ? index : chunks - 1];
+            const int at = index < chunks ? index : chunks - 1;
+            const std::uint16_t* source;
+            if constexpr (kContiguous) {
+                source = in + 8 * at;
+            } else {
+                const int per_row = d / 8;
+                source = in + (at / per_row) * row_stride + 8 * (at % per_row);
+            }
+            const uint4v loaded = *reinterpret_cast<const uint4v*>(source);
             chunk[c] = index < chunks ? loaded : uint4v{0u, 0u, 0u, 0u};
         }
 #pragma unroll
@@ -57,7 +69,7 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSid
         for (int e = 0; e < 8; ++e) absmax = fmaxf(absmax, static_cast<float>(magnitude[e]));
     } else {
         for (int index = t; index < count; index += kQuantThreads)
-            absmax = fmaxf(absmax, fabsf(half_bits_to_float(in[index])));
+            absmax = fmaxf(absmax, fabsf(half_bits_to_float(in[(index / d) * row_stride + index % d])));
     }
 
     absmax = wave_max(absmax);
@@ -85,7 +97,8 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSid
         }
     } else {
         for (int index = t; index < count; index += kQuantThreads)
-            out[index] = static_cast<std::int8_t>(quantize_value_recip(half_bits_to_float(in[index]), scale, recip));
+            out[index] = static_cast<std::int8_t>(
+                quantize_value_recip(half_bits_to_float(in[(index / d) * row_stride + index % d]), scale, recip));
     }
 }
 
@@ -103,26 +116,31 @@ hipError_t launch_quantize(const QuantSide& q, const QuantSide& k, int heads, in
     // The vector path reads 16-byte chunks of halves and writes 8-byte chunks
     // of int8; rows of d % 8 == 0 halves keep every block start aligned.
     bool vector = d % 8 == 0;
+    bool contiguous = true;
     for (const QuantSide* side : {&q, &k}) {
         if (side->blocks == 0) continue;
         vector = vector && aligned(side->x, 16) && aligned(side->x8, 8) &&
-                 (side->in_head_stride * 2) % 16 == 0;
+                 (side->in_head_stride * 2) % 16 == 0 && (side->in_row_stride * 2) % 16 == 0;
+        contiguous = contiguous && side->in_row_stride == d;
     }
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(heads));
-    if (vector)
-        quantize_blocks_kernel<true><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
+    if (vector && contiguous)
+        quantize_blocks_kernel<true, true><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
+    else if (vector)
+        quantize_blocks_kernel<true, false><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
     else
-        quantize_blocks_kernel<false><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
+        quantize_blocks_kernel<false, false><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
     return hipGetLastError();
 }
 
 QuantSide make_quant_side(const std::uint16_t* x, std::int8_t* x8, std::uint16_t* scales,
-                          std::int64_t head_stride, int rows, int block_rows) {
+                          std::int64_t head_stride, int rows, int block_rows, std::int64_t row_stride) {
     QuantSide side{};
     side.x = x;
     side.x8 = x8;
     side.scales = scales;
     side.in_head_stride = head_stride;
+    side.in_row_stride = row_stride;
     side.rows = rows;
     side.block_rows = block_rows;
     side.blocks = x ? (rows - 1) / block_rows + 1 : 0;
@@ -138,9 +156,34 @@ extern "C" int tilemix_quantize_qk(const std::uint16_t* Q, const std::uint16_t* 
     if (!Q || !K || !Q8 || !K8 || !q_scales || !k_scales || M <= 0 || N <= 0 || d <= 0)
         return hipErrorInvalidValue;
     if (d > tilemix::kMaxHeadDim) return hipErrorNotSupported;
-    const auto q = tilemix::make_quant_side(Q, Q8, q_scales, 0, M, tilemix::kQBlockRows);
-    const auto k = tilemix::make_quant_side(K, K8, k_scales, 0, N, tilemix::kKBlockRows);
+    const auto q = tilemix::make_quant_side(Q, Q8, q_scales, 0, M, tilemix::kQBlockRows, d);
+    const auto k = tilemix::make_quant_side(K, K8, k_scales, 0, N, tilemix::kKBlockRows, d);
     return tilemix::launch_quantize(q, k, 1, d, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tilemix_quantize_qk_strided(const std::uint16_t* Q, const std::uint16_t* K,
+                                           std::int8_t* Q8, std::int8_t* K8,
+                                           std::uint16_t* q_scales, std::uint16_t* k_scales,
+                                           int heads, int M, int N, int d,
+                                           std::int64_t q_head_stride, std::int64_t k_head_stride,
+                                           std::int64_t q_row_stride, std::int64_t k_row_stride,
+                                           void* stream) {
+    const bool q_side = Q || Q8 || q_scales;
+    const bool k_side = K || K8 || k_scales;
+    if ((q_side && (!Q || !Q8 || !q_scales)) || (k_side && (!K || !K8 || !k_scales)) ||
+        (!q_side && !k_side) || heads <= 0 || d <= 0 || (q_side && M <= 0) || (k_side && N <= 0))
+        return hipErrorInvalidValue;
+    const std::int64_t q_row = q_row_stride ? q_row_stride : d;
+    const std::int64_t k_row = k_row_stride ? k_row_stride : d;
+    if ((q_side && !tilemix::strided_heads_ok(heads, M, d, q_head_stride, q_row)) ||
+        (k_side && !tilemix::strided_heads_ok(heads, N, d, k_head_stride, k_row)))
+        return hipErrorInvalidValue;
+    if (d > tilemix::kMaxHeadDim) return hipErrorNotSupported;
+    const auto q = tilemix::make_quant_side(q_side ? Q : nullptr, Q8, q_scales, q_head_stride,
+                                            q_side ? M : 1, tilemix::kQBlockRows, q_row);
+    const auto k = tilemix::make_quant_side(k_side ? K : nullptr, K8, k_scales, k_head_stride,
+                                            k_side ? N : 1, tilemix::kKBlockRows, k_row);
+    return tilemix::launch_quantize(q, k, heads, d, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int tilemix_quantize_qk_batched(const std::uint16_t* Q, const std::uint16_t* K,
@@ -149,17 +192,6 @@ extern "C" int tilemix_quantize_qk_batched(const std::uint16_t* Q, const std::ui
                                            int heads, int M, int N, int d,
                                            std::int64_t q_head_stride, std::int64_t k_head_stride,
                                            void* stream) {
-    const bool q_side = Q || Q8 || q_scales;
-    const bool k_side = K || K8 || k_scales;
-    if ((q_side && (!Q || !Q8 || !q_scales)) || (k_side && (!K || !K8 || !k_scales)) ||
-        (!q_side && !k_side) || heads <= 0 || d <= 0 || (q_side && M <= 0) ||
-        (k_side && N <= 0) || (q_side && heads > 1 && q_head_stride < static_cast<std::int64_t>(M) * d) ||
-        (k_side && heads > 1 && k_head_stride < static_cast<std::int64_t>(N) * d))
-        return hipErrorInvalidValue;
-    if (d > tilemix::kMaxHeadDim) return hipErrorNotSupported;
-    const auto q = tilemix::make_quant_side(q_side ? Q : nullptr, Q8, q_scales, q_head_stride,
-                                            q_side ? M : 1, tilemix::kQBlockRows);
-    const auto k = tilemix::make_quant_side(k_side ? K : nullptr, K8, k_scales, k_head_stride,
-                                            k_side ? N : 1, tilemix::kKBlockRows);
-    return tilemix::launch_quantize(q, k, heads, d, static_cast<hipStream_t>(stream));
+    return tilemix_quantize_qk_strided(Q, K, Q8, K8, q_scales, k_scales, heads, M, N, d, q_head_stride,
+                                       k_head_stride, 0, 0, stream);
 }

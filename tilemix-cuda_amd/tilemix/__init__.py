@@ -23,6 +23,10 @@ from .api import (  # noqa: F401
     library_path,
     quantize_tilemix_qk,
     quantize_tilemix_qk_batched,
+    quantize_tilemix_qk_strided,
+    DTYPE_F32,
+    DTYPE_F16,
+    DTYPE_BF16,
     importance_workspace_bytes,
     routes_from_tiles,
     tiles_bernoulli,

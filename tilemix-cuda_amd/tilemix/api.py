@@ -29,6 +29,10 @@ def library_path() -> Path:
     return Path(override) if override else _PACKAGE_DIR / _LIB_NAME
 
 
+# Element types of O (include/tilemix_capi.h TILEMIX_DTYPE_*).
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+
+
 class _BatchedArgs(ctypes.Structure):
     _fields_ = [
         ("Q", ctypes.c_void_p), ("K", ctypes.c_void_p), ("V", ctypes.c_void_p), ("O", ctypes.c_void_p),
@@ -41,6 +45,8 @@ class _BatchedArgs(ctypes.Structure):
         ("key_tiles_per_group", ctypes.c_int), ("decoded_bits", ctypes.c_void_p),
         ("Q8", ctypes.c_void_p), ("K8", ctypes.c_void_p), ("q_scales", ctypes.c_void_p),
         ("k_scales", ctypes.c_void_p), ("score_dots", ctypes.c_void_p),
+        ("o_dtype", ctypes.c_int), ("q_row_stride", ctypes.c_int64), ("k_row_stride", ctypes.c_int64),
+        ("v_row_stride", ctypes.c_int64), ("o_row_stride", ctypes.c_int64),
     ]
 
 
@@ -70,6 +76,9 @@ def library() -> ctypes.CDLL:
         so.tilemix_attention_batched.restype = i32
         so.tilemix_quantize_qk_batched.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i64, i64, vp]
         so.tilemix_quantize_qk_batched.restype = i32
+        so.tilemix_quantize_qk_strided.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i64, i64, i64, i64,
+                                                   vp]
+        so.tilemix_quantize_qk_strided.restype = i32
         so.tilemix_routing_words_per_row_c.argtypes = [i32, i32]
         so.tilemix_routing_words_per_row_c.restype = sz
         so.tilemix_routing_word_count_c.argtypes = [i32, i32, i32]
@@ -199,6 +208,11 @@ class BatchedArgs:
     q_scales: Any = None
     k_scales: Any = None
     score_dots: Any = None
+    o_dtype: int = 0  # DTYPE_F32, DTYPE_F16 or DTYPE_BF16
+    q_row_stride: int = 0  # elements between rows of a head, 0 = d
+    k_row_stride: int = 0
+    v_row_stride: int = 0
+    o_row_stride: int = 0
 
     def to_c(self) -> _BatchedArgs:
         qn, kn = self.M * self.d, self.N * self.d
@@ -208,13 +222,22 @@ class BatchedArgs:
             self.o_head_stride or qn, ctypes.c_float(self.score_scale), int(self.causal),
             int(self.precise), int(self.quantize), _ptr(self.route_words), _ptr(self.skip_words),
             self.key_tiles_per_group, _ptr(self.decoded_bits), _ptr(self.Q8), _ptr(self.K8),
-            _ptr(self.q_scales), _ptr(self.k_scales), _ptr(self.score_dots))
+            _ptr(self.q_scales), _ptr(self.k_scales), _ptr(self.score_dots), int(self.o_dtype),
+            self.q_row_stride, self.k_row_stride, self.v_row_stride, self.o_row_stride)
 
 
 def attention_batched(args: BatchedArgs, stream=None) -> int:
     """tilemix_attention_batched; returns the hipError_t code."""
     c_args = args.to_c()
     return library().tilemix_attention_batched(ctypes.byref(c_args), _stream(stream))
+
+
+def quantize_tilemix_qk_strided(Q, K, Q8, K8, q_scales, k_scales, heads: int, M: int, N: int, d: int,
+                                q_head_stride: int = 0, k_head_stride: int = 0, q_row_stride: int = 0,
+                                k_row_stride: int = 0, stream=None) -> int:
+    return library().tilemix_quantize_qk_strided(
+        _ptr(Q), _ptr(K), _ptr(Q8), _ptr(K8), _ptr(q_scales), _ptr(k_scales), heads, M, N, d,
+        q_head_stride or M * d, k_head_stride or N * d, q_row_stride, k_row_stride, _stream(stream))
 
 
 def quantize_tilemix_qk_batched(Q, K, Q8, K8, q_scales, k_scales, heads: int, M: int, N: int, d: int,
