@@ -456,21 +456,28 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             }
             // ---- scores S^T[kb][b]: lane (g, i) holds query i, keys 16kb + 4g + r
             auto fp16_scores = [&]() {
+                // Feature chunk outermost (eight independent accumulator
+                // chains), the next chunk's K fragments read ahead.
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                    float4v acc0{0.0f, 0.0f, 0.0f, 0.0f}, acc1{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int b = 0; b < 2; ++b)
 #pragma unroll
-                    for (int dc = 0; dc < DC; ++dc) {
-                        const half8 kf = *reinterpret_cast<const half8*>(
+                    for (int kb = 0; kb < 4; ++kb) s[b][kb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+                half8 kf[2][4];
+                auto load_dc = [&](int dc, half8 (&dst)[4]) {
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+                        dst[kb] = *reinterpret_cast<const half8*>(
                             lds_k + (16 * kb + i) * L::kKStride + (32 * dc + 8 * g) * 2);
-                        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][dc], acc0, 0, 0, 0);
-                        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[1][dc], acc1, 0, 0, 0);
-                    }
-                    s[0][kb] = acc0;
-                    s[1][kb] = acc1;
-                    // Keep the scheduler from hoisting every K fragment read
-                    // of the tile (register pressure); the co-resident
-                    // workgroup hides the LDS latency instead.
+                };
+                load_dc(0, kf[0]);
+#pragma unroll
+                for (int dc = 0; dc < DC; ++dc) {
+                    if (dc + 1 < DC) load_dc(dc + 1, kf[(dc + 1) & 1]);
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int b = 0; b < 2; ++b)
+                            s[b][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc & 1][kb], qf[b][dc], s[b][kb], 0, 0, 0);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             };
@@ -513,19 +520,38 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 c = p.score_log2;
             } else if (wave_skip == 0 && wave_int8 == 0xfu) {
                 load_q8();
+                int4v acc[2][4];
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb) acc[b][kb] = int4v{0, 0, 0, 0};
+                int4v kf8[2][4];
+                auto load_m = [&](int m, int4v (&dst)[4]) {
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+                        dst[kb] = *reinterpret_cast<const int4v*>(lds_k8 + (16 * kb + i) * L::kK8Stride + 64 * m + 16 * g);
+                };
+                load_m(0, kf8[0]);
+#pragma unroll
+                for (int m = 0; m < kD8C; ++m) {
+                    if (m + 1 < kD8C) load_m(m + 1, kf8[(m + 1) & 1]);
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int b = 0; b < 2; ++b)
+                            acc[b][kb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf8[m & 1][kb], q8f[b][m], acc[b][kb], 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb) {
-                    int4v acc0, acc1;
-                    int8_dots(kb, acc0, acc1);
                     if (kDots && p.dots) {
-                        store_dots(kb, 0, acc0);
-                        store_dots(kb, 1, acc1);
+                        store_dots(kb, 0, acc[0][kb]);
+                        store_dots(kb, 1, acc[1][kb]);
                     }
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        s[0][kb][r] = static_cast<float>(acc0[r]);
-                        s[1][kb][r] = static_cast<float>(acc1[r]);
-                    }
+                    for (int b = 0; b < 2; ++b)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) s[b][kb][r] = static_cast<float>(acc[b][kb][r]);
                 }
                 c = k_factor;
             } else {
@@ -599,22 +625,37 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         half8 ph[2][2], pl[2][2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) softmax_tile<kFB, kPrecise>(st, b, s[b], c, ph[b], pl[b]);
+        {
+            // V^T fragments two 16-feature blocks at a time, the next pair
+            // read while this pair's MFMAs issue.
+            auto v_frag = [&](int ks, int fb) {
+                const unsigned char* v_lo = lds_v + (32 * ks + 4 * g + (i >> 2)) * L::kVStride + 8 * (i & 3);
+                return concat(read_tr16(v_lo + 32 * fb), read_tr16(v_lo + 16 * L::kVStride + 32 * fb));
+            };
+            constexpr int kPairs = kFB;  // (ks, fb pair) stages: 2 * kFB / 2
+            half8 vf[2][2];
+            vf[0][0] = v_frag(0, 0);
+            vf[0][1] = v_frag(0, kFB > 1 ? 1 : 0);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const unsigned char* v_lo = lds_v + (32 * ks + 4 * g + (i >> 2)) * L::kVStride + 8 * (i & 3);
-            const unsigned char* v_hi = v_lo + 16 * L::kVStride;
-#pragma unroll
-            for (int fb = 0; fb < kFB; ++fb) {
-                const half8 vf = concat(read_tr16(v_lo + 32 * fb), read_tr16(v_hi + 32 * fb));
-#pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    st.o[b][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[b][ks], st.o[b][fb], 0, 0, 0);
-                    if constexpr (kPrecise)
-                        st.o[b][fb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[b][ks], st.o[b][fb], 0, 0, 0);
+            for (int stage = 0; stage < kPairs; ++stage) {
+                const int ks = (2 * stage) / kFB, fb0 = (2 * stage) % kFB;
+                if (stage + 1 < kPairs) {
+                    const int ks_n = (2 * stage + 2) / kFB, fb_n = (2 * stage + 2) % kFB;
+                    vf[(stage + 1) & 1][0] = v_frag(ks_n, fb_n);
+                    vf[(stage + 1) & 1][1] = v_frag(ks_n, fb_n + 1 < kFB ? fb_n + 1 : fb_n);
                 }
-                if (fb % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    if (fb0 + h >= kFB) continue;
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        st.o[b][fb0 + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[stage & 1][h], ph[b][ks], st.o[b][fb0 + h], 0, 0, 0);
+                        if constexpr (kPrecise)
+                            st.o[b][fb0 + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[stage & 1][h], pl[b][ks], st.o[b][fb0 + h], 0, 0, 0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-
         }
         j = j_next;
     }
