@@ -88,56 +88,69 @@ struct RowState {
     float m[2];
 };
 
-// x[kb] holds the 16 scores of query row i of block b for keys 16kb + 4g + r.
-// c is the per-tile log2-domain factor (>= 0); explicit scores pass c = 1.
+// x[b][kb] holds the 16 scores of query row i of block b for keys
+// 16kb + 4g + r; c is the per-tile log2-domain factor (>= 0); explicit scores
+// pass c = 1. Both blocks of the wave are handled together: one pass of row
+// maxima (the cross-lane steps of the two blocks interleave) and one
+// wave-uniform branch for the rare rescale.
 template <int kFB, bool kPrecise>
-__device__ __forceinline__ void softmax_tile(RowState<kFB>& st, int b, float4v (&x)[4], float c,
-                                             half8 (&ph)[2], half8 (&pl)[2]) {
-    const float t0 = max3(max3(x[0][0], x[0][1], x[0][2]), x[0][3], x[1][3]);
-    const float t1 = max3(x[1][0], x[1][1], x[1][2]);
-    const float t2 = max3(max3(x[2][0], x[2][1], x[2][2]), x[2][3], x[3][3]);
-    const float t3 = max3(x[3][0], x[3][1], x[3][2]);
-    float tile = max3(max3(t0, t1, t2), t3, t3);
-    tile *= c;  // c >= 0 and rounding is monotone: max(x) * c == max(x * c)
-    tile = row_max4(tile);
-    const bool raise = tile > st.m[b] + kLazyRescale;
-    if (__any(raise)) {
-        // Rows with no visible key yet keep m = -inf (their sums are still 0).
-        const float m_new = fmaxf(st.m[b], tile);
-        const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(st.m[b] - m_new);
-        st.m[b] = m_new;
+__device__ __forceinline__ void softmax_tile(RowState<kFB>& st, const float4v (&x)[2][4], float c,
+                                             half8 (&ph)[2][2], half8 (&pl)[2][2]) {
+    float tile[2];
 #pragma unroll
-        for (int fb = 0; fb < kFB; ++fb) st.o[b][fb] *= alpha;
-        st.l[b] *= alpha;
+    for (int b = 0; b < 2; ++b) {
+        const float t0 = max3(max3(x[b][0][0], x[b][0][1], x[b][0][2]), x[b][0][3], x[b][1][3]);
+        const float t1 = max3(x[b][1][0], x[b][1][1], x[b][1][2]);
+        const float t2 = max3(max3(x[b][2][0], x[b][2][1], x[b][2][2]), x[b][2][3], x[b][3][3]);
+        const float t3 = max3(x[b][3][0], x[b][3][1], x[b][3][2]);
+        tile[b] = max3(max3(t0, t1, t2), t3, t3) * c;  // c >= 0: max(x) * c == max(x * c)
     }
-    // m == -inf only while every score seen, this tile included, is masked.
-    const float neg_m = st.m[b] == -INFINITY ? 0.0f : -st.m[b];
+    row_max4_pair(tile[0], tile[1]);
+    const bool raise0 = tile[0] > st.m[0] + kLazyRescale, raise1 = tile[1] > st.m[1] + kLazyRescale;
+    if (__any(raise0 || raise1)) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+        for (int b = 0; b < 2; ++b) {
+            // Rows with no visible key yet keep m = -inf (their sums are still 0).
+            const float m_new = fmaxf(st.m[b], tile[b]);
+            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(st.m[b] - m_new);
+            st.m[b] = m_new;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(x[2 * ks][r], c, neg_m));
-            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[2 * ks + 1][r], c, neg_m));
-            const _Float16 ha = static_cast<_Float16>(a), he = static_cast<_Float16>(e);
-            ph[ks][r] = ha;
-            ph[ks][4 + r] = he;
-            if constexpr (kPrecise) {
-                pl[ks][r] = static_cast<_Float16>(a - static_cast<float>(ha));
-                pl[ks][4 + r] = static_cast<_Float16>(e - static_cast<float>(he));
-            }
+            for (int fb = 0; fb < kFB; ++fb) st.o[b][fb] *= alpha;
+            st.l[b] *= alpha;
         }
-    // Row sum of exactly the fp16 probabilities P.V uses (exact fp32 sums of
-    // pairs, v_dot2_f32_f16 against 1), so the rounding of P cancels in O.
+    }
     const half2v one2{1.0f16, 1.0f16};
-    float sum = st.l[b];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int b = 0; b < 2; ++b) {
+        // m == -inf only while every score seen, this tile included, is masked.
+        const float neg_m = st.m[b] == -INFINITY ? 0.0f : -st.m[b];
 #pragma unroll
-        for (int k = 0; k < 8; k += 2) {
-            sum = __builtin_amdgcn_fdot2(half2v{ph[ks][k], ph[ks][k + 1]}, one2, sum, false);
-            if constexpr (kPrecise) sum = __builtin_amdgcn_fdot2(half2v{pl[ks][k], pl[ks][k + 1]}, one2, sum, false);
-        }
-    st.l[b] = sum;
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][2 * ks][r], c, neg_m));
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][2 * ks + 1][r], c, neg_m));
+                const _Float16 ha = static_cast<_Float16>(a), he = static_cast<_Float16>(e);
+                ph[b][ks][r] = ha;
+                ph[b][ks][4 + r] = he;
+                if constexpr (kPrecise) {
+                    pl[b][ks][r] = static_cast<_Float16>(a - static_cast<float>(ha));
+                    pl[b][ks][4 + r] = static_cast<_Float16>(e - static_cast<float>(he));
+                }
+            }
+        // Row sum of exactly the fp16 probabilities P.V uses (exact fp32 sums of
+        // pairs, v_dot2_f32_f16 against 1), so the rounding of P cancels in O.
+        float sum = st.l[b];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int k = 0; k < 8; k += 2) {
+                sum = __builtin_amdgcn_fdot2(half2v{ph[b][ks][k], ph[b][ks][k + 1]}, one2, sum, false);
+                if constexpr (kPrecise)
+                    sum = __builtin_amdgcn_fdot2(half2v{pl[b][ks][k], pl[b][ks][k + 1]}, one2, sum, false);
+            }
+        st.l[b] = sum;
+    }
 }
 
 template <int DC, bool kVector, bool kPrecise, bool kDots>
@@ -383,6 +396,16 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         __syncthreads();
     };
 
+    // The wave's quantized Q rows (INT8 operand), kept in registers.
+    int4v q8f[2][kD8C];
+    if (p.int8_operands) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int m = 0; m < kD8C; ++m)
+                q8f[b][m] = *reinterpret_cast<const int4v*>(
+                    lds_q8 + (wave * kRowsPerWave + 16 * b + i) * L::kQ8Stride + 64 * m + 16 * g);
+    }
     // ---------------------------------------------------------- key loop
     RowState<kFB> st;
 #pragma unroll
@@ -481,16 +504,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                     __builtin_amdgcn_sched_barrier(0);
                 }
             };
-            // The wave's quantized Q rows, loaded on tiles that have INT8 cells.
-            int4v q8f[2][kD8C];
-            auto load_q8 = [&]() {
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-#pragma unroll
-                    for (int m = 0; m < kD8C; ++m)
-                        q8f[b][m] = *reinterpret_cast<const int4v*>(
-                            lds_q8 + (wave * kRowsPerWave + 16 * b + i) * L::kQ8Stride + 64 * m + 16 * g);
-            };
+            auto load_q8 = [&]() {};
             // Exact int32 dots of key block kb for both query blocks.
             auto int8_dots = [&](int kb, int4v& acc0, int4v& acc1) {
                 acc0 = int4v{0, 0, 0, 0};
@@ -623,8 +637,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 
         // ---- online softmax, then O^T += V^T P^T and l += 1^T P^T
         half8 ph[2][2], pl[2][2];
-#pragma unroll
-        for (int b = 0; b < 2; ++b) softmax_tile<kFB, kPrecise>(st, b, s[b], c, ph[b], pl[b]);
+        softmax_tile<kFB, kPrecise>(st, s, c, ph, pl);
         {
             // V^T fragments two 16-feature blocks at a time, the next pair
             // read while this pair's MFMAs issue.

@@ -104,6 +104,18 @@ __device__ __forceinline__ float row_max4(float x) {
     permlane32_swap(c, e);
     return max3(c, e, e);
 }
+// row_max4 of two independent values, their cross-lane steps interleaved.
+__device__ __forceinline__ void row_max4_pair(float& x, float& y) {
+    float a = x, b = x, c = y, d = y;
+    permlane16_swap(a, b);
+    permlane16_swap(c, d);
+    float e = max3(a, b, b), f = e, h = max3(c, d, d), k = h;
+    permlane32_swap(e, f);
+    permlane32_swap(h, k);
+    x = max3(e, f, f);
+    y = max3(h, k, k);
+}
+
 __device__ __forceinline__ float row_sum4(float x) {
     float a = x, b = x;
     permlane16_swap(a, b);
