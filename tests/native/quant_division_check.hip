@@ -1,8 +1,11 @@
 // Exhaustive device check of the quantizer's division-free quotient
-// (tilemix_device.h: quotient / quantize_value_recip) against IEEE division
-// (quantize_value, built with -fhip-fp32-correctly-rounded-divide-sqrt):
-// for every positive finite fp16 block maximum a and every fp16 x with
-// |x| <= a, the fp32 quotients (as values) and the int8 results must agree.
+// (tilemix_device.h: quotient / quantize_value_recip / quantize_in_block /
+// quantize_half) against IEEE division (quantize_value, built with
+// -fhip-fp32-correctly-rounded-divide-sqrt): for every positive finite fp16
+// block maximum a and every fp16 x with |x| <= a, the fp32 quotients (as
+// values) and the int8 results must agree; quantize_half reads x from either
+// half of a word whose other half holds a different value. Also checks
+// pack_bytes against shifts for every int8 value in each byte position.
 // Prints "PASS <pairs>" or the first mismatches; exit code 0 on pass.
 #include "tilemix_device.h"
 
@@ -25,12 +28,31 @@ __global__ void check(unsigned long long* pairs, unsigned long long* bad, unsign
             const float fast = quotient(x, scale, recip);
             const int q_exact = quantize_value(x, scale);
             const int q_fast = quantize_value_recip(x, scale, recip);
+            const int q_block = quantize_in_block(x, scale, recip);
+            const unsigned bits = m | (sign << 15), other = bits ^ 0x5a5au;
+            const int q_lo = quantize_half<0>(bits | (other << 16), scale, recip);
+            const int q_hi = quantize_half<1>(other | (bits << 16), scale, recip);
             ++n;
             // Quotients compare as floats: x = -0 gives -0 by division and +0 here,
             // which quantize alike; every other quotient must match bit for bit.
-            if (exact != fast || q_exact != q_fast) {
+            if (exact != fast || q_exact != q_fast || q_exact != q_block || q_exact != q_lo || q_exact != q_hi) {
                 ++wrong;
                 if (atomicCAS(first, 0u, (a_bits << 16) | m | (sign << 15)) == 0u) {}
+            }
+        }
+    }
+    if (blockIdx.x == 0) {
+        // pack_bytes: every int8 value in each position beside distinct neighbours.
+        for (int v = -128 + static_cast<int>(threadIdx.x); v < 128; v += blockDim.x) {
+            const int a = v, b = -v - 1, c = v ^ 0x55, d = 127 - v;
+            const std::uint32_t shifted = (static_cast<std::uint32_t>(a) & 0xffu) |
+                                          ((static_cast<std::uint32_t>(b) & 0xffu) << 8) |
+                                          ((static_cast<std::uint32_t>(c) & 0xffu) << 16) |
+                                          (static_cast<std::uint32_t>(d) << 24);
+            ++n;
+            if (pack_bytes(a, b, c, d) != shifted || pack_bytes(d, c, b, a) != __builtin_bswap32(shifted)) {
+                ++wrong;
+                (void)atomicCAS(first, 0u, 0xffff0000u | (static_cast<unsigned>(v) & 0xffffu));
             }
         }
     }

@@ -5,7 +5,9 @@ round(x / scale) per element. The HIP kernels replace the division by the
 block's reciprocal plus one exact correction step; tests/native/
 quant_division_check.hip compares that with IEEE division on the device for
 every positive finite fp16 block maximum and every fp16 value not above it
-(about 1.0e9 pairs), as fp32 quotients and as int8 results.
+(about 1.0e9 pairs), as fp32 quotients and as int8 results, for each of the
+per-element forms the kernels use (quantize_value_recip, quantize_in_block
+and both lanes of quantize_half), and checks pack_bytes on every int8 value.
 """
 from __future__ import annotations
 
@@ -27,4 +29,5 @@ def test_division_free_quotient_is_exact(cuda):
     print(result.stdout, result.stderr, flush=True)
     assert result.returncode == 0, result.stdout + result.stderr
     assert result.stdout.startswith("PASS "), result.stdout
-    assert int(result.stdout.split()[1]) == 1007713278
+    # 1007713278 (absmax, x) pairs plus 256 pack_bytes values.
+    assert int(result.stdout.split()[1]) == 1007713278 + 256

@@ -238,7 +238,8 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                     int v[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
-                        v[e] = dc < DC ? quantize_value_recip(static_cast<float>(qf[b][dc < DC ? dc : 0][e]), scale, recip) : 0;
+                        v[e] = dc < DC && scale > 0.0f
+                            ? quantize_in_block(static_cast<float>(qf[b][dc < DC ? dc : 0][e]), scale, recip) : 0;
                     uint2v packed;
                     packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
                     packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);

@@ -14,18 +14,47 @@
 #include "tilemix_device.h"
 #include "tilemix_launch.h"
 
+#include <algorithm>
+
 namespace tilemix {
 namespace {
 
 constexpr int kQuantThreads = 256;
 constexpr int kQuantMaxChunks = (128 * 128 / 8) / kQuantThreads;  // 16-byte chunks per thread
 
+// Elementwise unsigned maximum of two pairs of 16-bit values.
+__device__ __forceinline__ unsigned max_u16x2(unsigned a, unsigned b) {
+    unsigned r;
+    asm("v_pk_max_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// Maximum over the wave's 64 lanes, returned in every lane: DPP steps inside
+// rows of 16 lanes (quad partners ^1 and ^2, then the mirrored lane within 8
+// and within 16), then v_permlane16_swap / v_permlane32_swap across rows
+// (inline assembly, s_nop 1 covering the VALU-write -> permlane-read hazard).
+__device__ __forceinline__ unsigned wave_max_bits(unsigned v) {
+    v = max(v, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xb1, 0xf, 0xf, false)));
+    v = max(v, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4e, 0xf, 0xf, false)));
+    v = max(v, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xf, 0xf, false)));
+    v = max(v, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x140, 0xf, 0xf, false)));
+    unsigned a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    v = max(a, b);
+    a = v;
+    b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return max(a, b);
+}
+
 // kContiguous: rows are d elements apart, so a block is one span of
 // rows * d halves; otherwise chunk c of the block is chunk c % (d / 8) of row
-// c / (d / 8).
-template <bool kVector, bool kContiguous>
+// c / (d / 8). kChunks: 16-byte chunks held per thread, enough for the
+// larger block of the launch (4 for 64 x 128 K blocks, 8 for 128 x 128 Q).
+template <bool kVector, bool kContiguous, int kChunks = kQuantMaxChunks>
 __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSide q, QuantSide k, int d) {
     __shared__ float partial[kQuantThreads / kWave];
+    __shared__ unsigned partial_bits[kQuantThreads / kWave];
     const bool is_q = static_cast<int>(blockIdx.x) < q.blocks;
     const QuantSide side = is_q ? q : k;
     const int block = is_q ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x) - q.blocks;
@@ -39,17 +68,14 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSid
                        static_cast<std::int64_t>(first) * d;
     const int t = threadIdx.x;
 
-    float absmax = 0.0f;
-    uint4v chunk[kQuantMaxChunks];
+    uint4v chunk[kChunks];
     const int chunks = count / 8;
+    float absmax = 0.0f;
     if constexpr (kVector) {
-        half8 magnitude{};  // elementwise maxima of |x| (fp16 max ignores NaN, as fmaxf does)
-        const uint4v sign_off{0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};
-        // Every lane issues all loads, past-the-end lanes from the block's last
-        // chunk (chunks >= 1 since d % 8 == 0), and keeps zeros instead; loads
-        // under a branch would serialise behind one wait each.
+        // Chunks past the block's end load its last chunk again (in-block
+        // values, which leave the maximum unchanged; they are not stored).
 #pragma unroll
-        for (int c = 0; c < kQuantMaxChunks; ++c) {
+        for (int c = 0; c < kChunks; ++c) {
             const int index = t + c * kQuantThreads;
             const int at = index < chunks ? index : chunks - 1;
             const std::uint16_t* source;
@@ -59,40 +85,71 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_blocks_kernel(QuantSid
                 const int per_row = d / 8;
                 source = in + (at / per_row) * row_stride + 8 * (at % per_row);
             }
-            const uint4v loaded = *reinterpret_cast<const uint4v*>(source);
-            chunk[c] = index < chunks ? loaded : uint4v{0u, 0u, 0u, 0u};
+            chunk[c] = *reinterpret_cast<const uint4v*>(source);
         }
+        // |x| as fp16 bit patterns: unsigned order is float order for them,
+        // NaN patterns (> 0x7c00) sorting above +inf.
+        unsigned top = 0;
 #pragma unroll
-        for (int c = 0; c < kQuantMaxChunks; ++c)
-            magnitude = __builtin_elementwise_max(magnitude, __builtin_bit_cast(half8, chunk[c] & sign_off));
+        for (int c = 0; c < kChunks; ++c)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) absmax = fmaxf(absmax, static_cast<float>(magnitude[e]));
+            for (int w = 0; w < 4; ++w) top = max_u16x2(top, chunk[c][w] & 0x7fff7fffu);
+        unsigned bits = wave_max_bits(max(top & 0xffffu, top >> 16));
+        if ((t & (kWave - 1)) == 0) partial_bits[t / kWave] = bits;
+        __syncthreads();
+        bits = max(max(partial_bits[0], partial_bits[1]), max(partial_bits[2], partial_bits[3]));
+        if (bits > 0x7c00u) {
+            // A NaN in the block: the maximum skips NaNs, as fmaxf does.
+            unsigned clean = 0;
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const unsigned h = (chunk[c][e / 2] >> (16 * (e % 2))) & 0x7fffu;
+                    clean = h <= 0x7c00u ? max(clean, h) : clean;
+                }
+            clean = wave_max_bits(clean);
+            __syncthreads();
+            if ((t & (kWave - 1)) == 0) partial_bits[t / kWave] = clean;
+            __syncthreads();
+            bits = max(max(partial_bits[0], partial_bits[1]), max(partial_bits[2], partial_bits[3]));
+        }
+        absmax = half_bits_to_float(static_cast<std::uint16_t>(bits));
     } else {
         for (int index = t; index < count; index += kQuantThreads)
             absmax = fmaxf(absmax, fabsf(half_bits_to_float(in[(index / d) * row_stride + index % d])));
+        absmax = wave_max(absmax);
+        if ((t & (kWave - 1)) == 0) partial[t / kWave] = absmax;
+        __syncthreads();
+        absmax = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
     }
-
-    absmax = wave_max(absmax);
-    if ((t & (kWave - 1)) == 0) partial[t / kWave] = absmax;
-    __syncthreads();
-    absmax = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
     const float scale = block_scale(absmax);
     const float recip = 1.0f / scale;  // used only when scale > 0
     if (t == 0) side.scales[head * side.blocks + block] = float_to_half_bits(scale);
 
     if constexpr (kVector) {
+        if (scale > 0.0f) {
 #pragma unroll
-        for (int c = 0; c < kQuantMaxChunks; ++c) {
-            const int index = t + c * kQuantThreads;
-            if (index < chunks) {
-                const half8 h = __builtin_bit_cast(half8, chunk[c]);
-                int v[8];
+            for (int c = 0; c < kChunks; ++c) {
+                const int index = t + c * kQuantThreads;
+                if (index < chunks) {
+                    int v[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = quantize_value_recip(static_cast<float>(h[e]), scale, recip);
-                uint2v packed;
-                packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
-                packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);
-                reinterpret_cast<uint2v*>(out)[index] = packed;
+                    for (int e = 0; e < 8; e += 2) {
+                        v[e] = quantize_half<0>(chunk[c][e / 2], scale, recip);
+                        v[e + 1] = quantize_half<1>(chunk[c][e / 2], scale, recip);
+                    }
+                    uint2v packed;
+                    packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
+                    packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);
+                    reinterpret_cast<uint2v*>(out)[index] = packed;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) {
+                const int index = t + c * kQuantThreads;
+                if (index < chunks) reinterpret_cast<uint2v*>(out)[index] = uint2v{0u, 0u};
             }
         }
     } else {
@@ -124,8 +181,17 @@ hipError_t launch_quantize(const QuantSide& q, const QuantSide& k, int heads, in
         contiguous = contiguous && side->in_row_stride == d;
     }
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(heads));
-    if (vector && contiguous)
+    // Chunks of 16 bytes per thread the larger block of the launch needs.
+    std::int64_t need = 0;
+    for (const QuantSide* side : {&q, &k})
+        if (side->blocks) need = std::max<std::int64_t>(need, static_cast<std::int64_t>(side->block_rows) * d / 8);
+    const bool small = need <= 4 * kQuantThreads;
+    if (vector && contiguous && small)
+        quantize_blocks_kernel<true, true, 4><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
+    else if (vector && contiguous)
         quantize_blocks_kernel<true, true><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
+    else if (vector && small)
+        quantize_blocks_kernel<true, false, 4><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
     else if (vector)
         quantize_blocks_kernel<true, false><<<grid, kQuantThreads, 0, stream>>>(q, k, d);
     else

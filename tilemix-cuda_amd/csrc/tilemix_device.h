@@ -71,6 +71,34 @@ __device__ __forceinline__ int quantize_value_recip(float x, float scale, float 
     return rounded < -127 ? -127 : (rounded > 127 ? 127 : rounded);
 }
 
+// quantize_value_recip for an element of its own block with a positive scale
+// (|x| <= absmax, scale = absmax / 127 > 0): |x / scale| <= 127 (1 + 2^-24),
+// so the shifted quotient truncates into [-127, 127] and the clamp is never
+// taken; a NaN quotient converts to 0 either way. The exhaustive device check
+// in tests/native/quant_division_check.hip compares it with quantize_value.
+__device__ __forceinline__ int quantize_in_block(float x, float scale, float recip) {
+    const float normalized = quotient(x, scale, recip);
+    return static_cast<int>(normalized + __builtin_copysignf(0.5f, normalized));
+}
+
+// quantize_in_block of half kHalf (0 = low) of two packed fp16 elements. The
+// first product is read straight from the fp16 half (v_fma_mix_f32 with a
+// zero addend: RN(x * recip), which differs from the f32 product only in the
+// sign of a zero product, and a zero quotient rounds to 0 either way); the
+// exhaustive device check in tests/native/quant_division_check.hip compares
+// both halves with quantize_value.
+template <int kHalf>
+__device__ __forceinline__ int quantize_half(std::uint32_t pair, float scale, float recip) {
+    float y;
+    if constexpr (kHalf == 0)
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(y) : "v"(pair), "v"(recip));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(y) : "v"(pair), "v"(recip));
+    const float x = half_bits_to_float(static_cast<std::uint16_t>(pair >> (16 * kHalf)));
+    const float q = __builtin_fmaf(__builtin_fmaf(-scale, y, x), recip, y);
+    return static_cast<int>(q + __builtin_copysignf(0.5f, q));
+}
+
 __device__ __forceinline__ float wave_max(float value) {
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset));
@@ -78,9 +106,11 @@ __device__ __forceinline__ float wave_max(float value) {
 }
 
 // Packs four quantized values (low byte first) into one 32-bit word.
+// Three v_perm_b32: (a, b) and (c, d) low bytes into halves, then the halves.
 __device__ __forceinline__ std::uint32_t pack_bytes(int a, int b, int c, int d) {
-    return (static_cast<std::uint32_t>(a) & 0xffu) | ((static_cast<std::uint32_t>(b) & 0xffu) << 8) |
-           ((static_cast<std::uint32_t>(c) & 0xffu) << 16) | (static_cast<std::uint32_t>(d) << 24);
+    const std::uint32_t lo = __builtin_amdgcn_perm(static_cast<std::uint32_t>(b), static_cast<std::uint32_t>(a), 0x0c0c0400u);
+    const std::uint32_t hi = __builtin_amdgcn_perm(static_cast<std::uint32_t>(d), static_cast<std::uint32_t>(c), 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 }  // namespace tilemix
