@@ -230,7 +230,10 @@ void tmo_quantize(const uint16_t* x, int rows, int d, int block_rows,
                 const size_t index = (size_t)row * d + f;
                 const float normalized = scale == 0.0f ? 0.0f : tmo_half_to_float(x[index]) / scale;
                 const float shifted = normalized < 0.0f ? normalized - 0.5f : normalized + 0.5f;
-                int rounded = (int)shifted; /* truncation toward zero */
+                /* __float2int_rz (src/tilemix.cu:45): truncation toward zero, NaN
+                   (x NaN, or x = +-inf in a block whose maximum is inf) -> 0;
+                   C's (int) of a NaN is undefined, so that case is spelled out. */
+                int rounded = shifted != shifted ? 0 : (int)shifted;
                 if (rounded > 127) rounded = 127;
                 if (rounded < -127) rounded = -127;
                 out[index] = (int8_t)rounded;

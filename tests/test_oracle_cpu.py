@@ -242,6 +242,25 @@ def test_quantizer_tiny_and_max_range():
     assert from_bits(scales).tolist() == [516.0]
 
 
+def test_quantizer_special_values():
+    # src/tilemix.cu:27,45: the block maximum skips NaNs (fmaxf), and the
+    # saturating __float2int_rz turns a NaN quotient into 0, so NaN elements,
+    # and +-inf elements of a block whose maximum is inf (inf / inf), give 0.
+    nan, neg_nan, inf, neg_inf = 0x7E00, 0xFE00, 0x7C00, 0xFC00
+    x = as_f16_bits(np.full((320, 8), 0.5))
+    x[3, 2], x[7, 1] = nan, neg_nan          # block 0: NaNs among 0.5s
+    x[64 + 5, 4] = inf                       # block 1: an inf maximum
+    x[128:192] = nan                         # block 2: NaN only
+    x[192 + 1, 0], x[192 + 9, 6] = nan, neg_inf  # block 3: NaN and -inf
+    x[256:320] = 0x8000                      # block 4: -0 only
+    values, scales = oracle.quantize(x, 64)
+    assert scales.tolist() == [int(as_f16_bits(np.float32(0.5) / np.float32(127.0))), inf, 0, inf, 0]
+    expected = np.zeros((320, 8), dtype=np.int8)
+    expected[:64] = 127
+    expected[3, 2] = expected[7, 1] = 0
+    assert np.array_equal(values, expected)
+
+
 @pytest.mark.parametrize("rows,d,block", [(137, 31, 128), (73, 31, 64), (300, 128, 128), (257, 64, 64),
                                           (131, 17, 64), (5, 1, 64)])
 def test_quantizer_brute_force_and_invariants(rows, d, block):
