@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     __shared__ __attribute__((aligned(16))) unsigned char smem[L::kSmemBytes];
     // Quantized Q rows (B operand of the INT8 MFMA), read on INT8 tiles only.
     __shared__ __attribute__((aligned(16))) unsigned char lds_q8[L::kQ8Bytes];
-    __shared__ float group_max[kWavesPerGroup];
+    __shared__ unsigned group_bits[kWavesPerGroup];
     unsigned char* const lds_k = smem;
     unsigned char* const lds_v = smem + L::kKBytes;
     unsigned char* const lds_k8 = smem + L::kKBytes + L::kVBytes;
@@ -211,19 +211,45 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     float q_scale = 0.0f;
     if (p.int8_operands) {
         if (p.fuse_q_quant) {
-            // The workgroup's rows are exactly one 128-row Q block.
-            float absmax = 0.0f;
+            // The workgroup's rows are exactly one 128-row Q block. Its
+            // maximum |x| as fp16 bit patterns: unsigned order is float order
+            // for them, NaN patterns (> 0x7c00) sorting above +inf.
+            unsigned top = 0;
 #pragma unroll
             for (int b = 0; b < 2; ++b)
 #pragma unroll
-                for (int dc = 0; dc < DC; ++dc)
+                for (int dc = 0; dc < DC; ++dc) {
+                    const uint4v words = __builtin_bit_cast(uint4v, qf[b][dc]);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) absmax = fmaxf(absmax, fabsf(static_cast<float>(qf[b][dc][e])));
-            absmax = wave_max(absmax);
-            if (lane == 0) group_max[wave] = absmax;
+                    for (int w = 0; w < 4; ++w) top = max_u16x2(top, words[w] & 0x7fff7fffu);
+                }
+            unsigned bits = wave_max_bits(max(top & 0xffffu, top >> 16));
+            if (lane == 0) group_bits[wave] = bits;
             __syncthreads();
-            absmax = fmaxf(fmaxf(group_max[0], group_max[1]), fmaxf(group_max[2], group_max[3]));
-            const float scale = block_scale(absmax);
+            bits = max(max(group_bits[0], group_bits[1]), max(group_bits[2], group_bits[3]));
+            if (bits > 0x7c00u) {
+                // A NaN in the block: the maximum skips NaNs, as fmaxf does.
+                unsigned clean = 0;
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            // The element is copied out first: __builtin_bit_cast
+                            // applied to a vector element expression reads
+                            // element 0 under this compiler.
+                            const _Float16 x = qf[b][dc][e];
+                            const unsigned h = __builtin_bit_cast(std::uint16_t, x) & 0x7fffu;
+                            clean = h <= 0x7c00u ? max(clean, h) : clean;
+                        }
+                clean = wave_max_bits(clean);
+                __syncthreads();
+                if (lane == 0) group_bits[wave] = clean;
+                __syncthreads();
+                bits = max(max(group_bits[0], group_bits[1]), max(group_bits[2], group_bits[3]));
+            }
+            const float scale = block_scale(half_bits_to_float(static_cast<std::uint16_t>(bits)));
             const float recip = 1.0f / scale;
             const _Float16 stored = static_cast<_Float16>(scale);
             q_scale = static_cast<float>(stored);
@@ -235,14 +261,18 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 const int row = q0 + local;
 #pragma unroll
                 for (int dc = 0; dc < 2 * kD8C; ++dc) {
-                    int v[8];
+                    uint2v packed{0u, 0u};
+                    if (dc < DC && scale > 0.0f) {
+                        const uint4v words = __builtin_bit_cast(uint4v, qf[b][dc < DC ? dc : 0]);
+                        int v[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        v[e] = dc < DC && scale > 0.0f
-                            ? quantize_in_block(static_cast<float>(qf[b][dc < DC ? dc : 0][e]), scale, recip) : 0;
-                    uint2v packed;
-                    packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
-                    packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);
+                        for (int w = 0; w < 4; ++w) {
+                            v[2 * w] = quantize_half<0>(words[w], scale, recip);
+                            v[2 * w + 1] = quantize_half<1>(words[w], scale, recip);
+                        }
+                        packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
+                        packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);
+                    }
                     const int feature = 32 * dc + 8 * g;
                     *reinterpret_cast<uint2v*>(lds_q8 + local * L::kQ8Stride + feature) = packed;
                     if (p.q8_out && row < M && feature < d) {
@@ -251,7 +281,8 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                         if constexpr (kVector) {
                             *reinterpret_cast<uint2v*>(dst) = packed;
                         } else {
-                            for (int e = 0; e < 8 && feature + e < d; ++e) dst[e] = static_cast<std::int8_t>(v[e]);
+                            for (int e = 0; e < 8 && feature + e < d; ++e)
+                                dst[e] = static_cast<std::int8_t>(packed[e / 4] >> (8 * (e % 4)));
                         }
                     }
                 }

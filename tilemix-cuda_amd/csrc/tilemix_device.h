@@ -99,6 +99,31 @@ __device__ __forceinline__ int quantize_half(std::uint32_t pair, float scale, fl
     return static_cast<int>(q + __builtin_copysignf(0.5f, q));
 }
 
+// Elementwise unsigned maximum of two pairs of 16-bit values.
+__device__ __forceinline__ unsigned max_u16x2(unsigned a, unsigned b) {
+    unsigned r;
+    asm("v_pk_max_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// Maximum over the wave's 64 lanes, returned in every lane: DPP steps inside
+// rows of 16 lanes (quad partners ^1 and ^2, then the mirrored lane within 8
+// and within 16), then v_permlane16_swap / v_permlane32_swap across rows
+// (inline assembly, s_nop 1 covering the VALU-write -> permlane-read hazard).
+__device__ __forceinline__ unsigned wave_max_bits(unsigned v) {
+    v = max(v, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xb1, 0xf, 0xf, false)));
+    v = max(v, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4e, 0xf, 0xf, false)));
+    v = max(v, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x141, 0xf, 0xf, false)));
+    v = max(v, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x140, 0xf, 0xf, false)));
+    unsigned a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    v = max(a, b);
+    a = v;
+    b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return max(a, b);
+}
+
 __device__ __forceinline__ float wave_max(float value) {
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset));
