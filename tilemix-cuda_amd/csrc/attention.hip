@@ -17,12 +17,12 @@
 //    v_mfma_f32_16x16x32_f16; the V^T operand is read from the row-major V
 //    tile in LDS with ds_read_b64_tr_b16, which transposes 16-bit elements
 //    across each 16-lane group. Key order inside a 32-key MFMA step is
-//    permuted identically on both operands. Row sums add exactly the fp16
-//    probabilities P.V uses (v_dot2_f32_f16 against 1), per lane, reduced
-//    over the row's lanes once at the end.
+//    permuted identically on both operands. Row sums are the same MFMA with
+//    a block of ones in place of V^T (ones^T P^T): they add exactly the fp16
+//    probabilities P.V uses, over all of the row's keys, on the matrix core
+//    instead of the VALU.
 //  * K, K8 and V tiles move HBM -> LDS with buffer_load ... lds (no VGPR
-//    staging): per-lane offsets into the padded, bank-conflict-free LDS rows
-//    are computed once, each tile only changes a scalar offset, and rows past
+//    staging): per-lane offsets into the padded LDS rows are computed once, each tile only changes a scalar offset, and rows past
 //    the end of the head read as zero. The V tile is fetched while the
 //    scores are computed and the next K tile while softmax and P.V run, with
 //    two barriers per tile and 44 KiB of LDS so two workgroups share a CU.
@@ -57,8 +57,10 @@ struct Layout {
     static constexpr int kD8C = (DC + 1) / 2;      // 64-feature chunks, int8 path
     static constexpr int kDP8 = 64 * kD8C;
     static constexpr int kFB = kDP / 16;           // 16-feature output blocks
-    // Row strides pad each row by 16 (K, K8) or 32 (V) bytes so that the
-    // 16 rows an MFMA operand read touches start in distinct LDS banks.
+    // Row strides pad each row by 16 (K, K8) or 32 (V) bytes. The transposed
+    // V reads are then free of bank conflicts; the K / K8 fragment reads see
+    // two-way conflicts, which measured cheaper than a 32-byte pad (more DMA
+    // lanes per tile).
     static constexpr int kKStride = kDP * 2 + 16;
     static constexpr int kVStride = kDP * 2 + 32;
     static constexpr int kK8Stride = kDP8 + 16;
@@ -84,7 +86,7 @@ struct Layout {
 template <int kFB>
 struct RowState {
     float4v o[2][kFB];  // O^T accumulators: lane (g, i) holds O[row i][16fb + 4g + r]
-    float l[2];         // this lane's share of the row sum (its keys)
+    float4v l[2];       // row sums of P (ones^T P^T): every element holds row i's sum
     float m[2];
 };
 
@@ -119,7 +121,6 @@ __device__ __forceinline__ void softmax_tile(RowState<kFB>& st, const float4v (&
             st.l[b] *= alpha;
         }
     }
-    const half2v one2{1.0f16, 1.0f16};
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         // m == -inf only while every score seen, this tile included, is masked.
@@ -138,18 +139,6 @@ __device__ __forceinline__ void softmax_tile(RowState<kFB>& st, const float4v (&
                     pl[b][ks][4 + r] = static_cast<_Float16>(e - static_cast<float>(he));
                 }
             }
-        // Row sum of exactly the fp16 probabilities P.V uses (exact fp32 sums of
-        // pairs, v_dot2_f32_f16 against 1), so the rounding of P cancels in O.
-        float sum = st.l[b];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int k = 0; k < 8; k += 2) {
-                sum = __builtin_amdgcn_fdot2(half2v{ph[b][ks][k], ph[b][ks][k + 1]}, one2, sum, false);
-                if constexpr (kPrecise)
-                    sum = __builtin_amdgcn_fdot2(half2v{pl[b][ks][k], pl[b][ks][k + 1]}, one2, sum, false);
-            }
-        st.l[b] = sum;
     }
 }
 
@@ -444,10 +433,11 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
         for (int fb = 0; fb < kFB; ++fb) st.o[b][fb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-        st.l[b] = 0.0f;
+        st.l[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
         st.m[b] = -INFINITY;
     }
     const bool positive_scale = p.score_scale >= 0.0f;
+    const half8 ones{1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
 
     const int key_tiles64 = (N - 1) / kTileKeys + 1;
     int tiles = key_tiles64;
@@ -699,6 +689,15 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                             st.o[b][fb0 + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[stage & 1][h], pl[b][ks], st.o[b][fb0 + h], 0, 0, 0);
                     }
                 }
+                if (fb0 == 0) {
+                    // Row sums of exactly the fp16 P the P.V MFMAs use.
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph[b][ks], st.l[b], 0, 0, 0);
+                        if constexpr (kPrecise)
+                            st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pl[b][ks], st.l[b], 0, 0, 0);
+                    }
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -717,7 +716,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     // ---------------------------------------------------------- epilogue
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-        const float l = row_sum4(st.l[b]);  // the row's four lanes: i, i + 16, i + 32, i + 48
+        const float l = st.l[b][0];
         const float inverse = l > 0.0f ? 1.0f / l : 0.0f;
         const int row = qw + 16 * b + i;
         if (row >= M) continue;

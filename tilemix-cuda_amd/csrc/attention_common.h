@@ -86,7 +86,7 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
 // Cross-lane exchange without LDS: with a == b == x on entry,
 // v_permlane16_swap leaves a = x of rows {0, 0, 2, 2} and b = x of rows
 // {1, 1, 3, 3} (rows of 16 lanes); v_permlane32_swap leaves a = x of the lower
-// half in both halves and b = x of the upper half. So max(a, b) / a + b is
+// half in both halves and b = x of the upper half. So max(a, b) is
 // the butterfly step with partner lane ^ 16 / ^ 32. Inline assembly because
 // the compiler builtins for these swaps get folded as if both results were
 // the same value; s_nop 1 covers the VALU-write -> permlane-read hazard.
@@ -96,7 +96,7 @@ __device__ __forceinline__ void permlane16_swap(float& a, float& b) {
 __device__ __forceinline__ void permlane32_swap(float& a, float& b) {
     asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
-// Maximum / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row).
+// Maximum over lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row).
 __device__ __forceinline__ float row_max4(float x) {
     float a = x, b = x;
     permlane16_swap(a, b);
@@ -116,13 +116,6 @@ __device__ __forceinline__ void row_max4_pair(float& x, float& y) {
     y = max3(h, k, k);
 }
 
-__device__ __forceinline__ float row_sum4(float x) {
-    float a = x, b = x;
-    permlane16_swap(a, b);
-    float c = a + b, e = c;
-    permlane32_swap(c, e);
-    return c + e;
-}
 
 // ds_read_b64_tr_b16: within each 16-lane group, element e of lane i comes
 // from lane 4e + i / 4, element i % 4 of that lane's 8-byte row piece.
