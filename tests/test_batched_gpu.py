@@ -192,6 +192,8 @@ BATCH_CASES = [
     (2, 129, 4099, 64, 3, False, 0.0),
     (3, 260, 260, 96, 1, True, 0.4),
     (1, 4096, 4096, 128, 2, True, 0.0),
+    (2, 77, 333, 128, 1, True, 0.3),   # causal with fewer queries than keys
+    (2, 500, 130, 64, 2, True, 0.0),   # causal with more queries than keys
 ]
 
 
