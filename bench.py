@@ -17,8 +17,16 @@ INT8/FP16 MFMA peak of the same op mix. ``cpu_baseline`` times the CPU PyTorch
 restatement of the reference's CPU path (python/reference_attention.py) on a
 bounded sample of heads on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--precise]
-                       [--no-check] [--no-cpu-baseline]
+Warm-up: the W requested steps, then more untimed steps until at least
+--min-warmup-ms of wall time has passed since warm-up began. An MI355X
+raises its clock over the first tens of milliseconds of sustained work (the
+headline attention launch goes from about 0.39 ms to 0.31 ms after roughly
+50 ms), so a few steps alone would time the ramp rather than the sustained
+rate. The JSON line reports W as requested and the steps actually run; the
+timed region is exactly K steps either way.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--min-warmup-ms T] [--config 3]
+                       [--precise] [--no-check] [--no-cpu-baseline]
 """
 from __future__ import annotations
 
@@ -44,6 +52,9 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--min-warmup-ms", type=float, default=150.0,
+                   help="keep running untimed steps after the W warm-up steps until this much wall "
+                        "time has passed since warm-up began (0 disables)")
     p.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
     p.add_argument("--seed", type=int, default=20261201)
     p.add_argument("--precise", action="store_true", help="split-precision P.V (fp32-level accuracy)")
@@ -106,9 +117,19 @@ def main() -> int:
             events[1].record(stream)
 
     with torch.cuda.stream(stream):
+        warm_start = time.perf_counter()
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
+        warmup_run = args.warmup
+        while (time.perf_counter() - warm_start) * 1e3 < args.min_warmup_ms and warmup_run < 100000:
+            for _ in range(8):
+                step()
+            warmup_run += 8
+            torch.cuda.synchronize()
+        warmup_ms = (time.perf_counter() - warm_start) * 1e3
+        log(f"warm-up: {warmup_run} steps in {warmup_ms:.1f} ms ({args.warmup} requested, "
+            f"minimum {args.min_warmup_ms:g} ms)")
         pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                  for _ in range(args.steps)]
         torch.cuda.synchronize()
@@ -142,6 +163,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warmup_run,
+        "warmup_ms": round(warmup_ms, 1),
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
