@@ -470,9 +470,10 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     int j = next_tile(0);
     if (j < tiles) issue_k(j, needs16(cur_int8, cur_skip), cur_int8 != 0);
 
-    // One iteration per visible tile; the accumulator update at its end runs
-    // on every wave (inactive waves add zero probabilities), which keeps the
-    // O / l / m state on a single straight-line path through the loop.
+    // One iteration per visible tile. A wave with no visible key in the tile
+    // (rows above a causal diagonal, or all its cells skipped) takes part in
+    // the tile's loads and barriers only: its probabilities would all be 0,
+    // so the softmax and P.V would leave m, l and O unchanged.
     while (j < tiles) {
         const int k0 = j * kTileKeys;
         const std::uint32_t int8_mask = cur_int8, skip_mask = cur_skip;
@@ -658,47 +659,49 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         if (j_next < tiles) issue_k(j_next, needs16(cur_int8, cur_skip), cur_int8 != 0);
 
         // ---- online softmax, then O^T += V^T P^T and l += 1^T P^T
-        half8 ph[2][2], pl[2][2];
-        softmax_tile<kFB, kPrecise>(st, s, c, ph, pl);
-        {
-            // V^T fragments two 16-feature blocks at a time, the next pair
-            // read while this pair's MFMAs issue.
-            auto v_frag = [&](int ks, int fb) {
-                const unsigned char* v_lo = lds_v + (32 * ks + 4 * g + (i >> 2)) * L::kVStride + 8 * (i & 3);
-                return concat(read_tr16(v_lo + 32 * fb), read_tr16(v_lo + 16 * L::kVStride + 32 * fb));
-            };
-            constexpr int kPairs = kFB;  // (ks, fb pair) stages: 2 * kFB / 2
-            half8 vf[2][2];
-            vf[0][0] = v_frag(0, 0);
-            vf[0][1] = v_frag(0, kFB > 1 ? 1 : 0);
+        if (active) {
+            half8 ph[2][2], pl[2][2];
+            softmax_tile<kFB, kPrecise>(st, s, c, ph, pl);
+            {
+                // V^T fragments two 16-feature blocks at a time, the next pair
+                // read while this pair's MFMAs issue.
+                auto v_frag = [&](int ks, int fb) {
+                    const unsigned char* v_lo = lds_v + (32 * ks + 4 * g + (i >> 2)) * L::kVStride + 8 * (i & 3);
+                    return concat(read_tr16(v_lo + 32 * fb), read_tr16(v_lo + 16 * L::kVStride + 32 * fb));
+                };
+                constexpr int kPairs = kFB;  // (ks, fb pair) stages: 2 * kFB / 2
+                half8 vf[2][2];
+                vf[0][0] = v_frag(0, 0);
+                vf[0][1] = v_frag(0, kFB > 1 ? 1 : 0);
 #pragma unroll
-            for (int stage = 0; stage < kPairs; ++stage) {
-                const int ks = (2 * stage) / kFB, fb0 = (2 * stage) % kFB;
-                if (stage + 1 < kPairs) {
-                    const int ks_n = (2 * stage + 2) / kFB, fb_n = (2 * stage + 2) % kFB;
-                    vf[(stage + 1) & 1][0] = v_frag(ks_n, fb_n);
-                    vf[(stage + 1) & 1][1] = v_frag(ks_n, fb_n + 1 < kFB ? fb_n + 1 : fb_n);
-                }
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    if (fb0 + h >= kFB) continue;
-#pragma unroll
-                    for (int b = 0; b < 2; ++b) {
-                        st.o[b][fb0 + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[stage & 1][h], ph[b][ks], st.o[b][fb0 + h], 0, 0, 0);
-                        if constexpr (kPrecise)
-                            st.o[b][fb0 + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[stage & 1][h], pl[b][ks], st.o[b][fb0 + h], 0, 0, 0);
+                for (int stage = 0; stage < kPairs; ++stage) {
+                    const int ks = (2 * stage) / kFB, fb0 = (2 * stage) % kFB;
+                    if (stage + 1 < kPairs) {
+                        const int ks_n = (2 * stage + 2) / kFB, fb_n = (2 * stage + 2) % kFB;
+                        vf[(stage + 1) & 1][0] = v_frag(ks_n, fb_n);
+                        vf[(stage + 1) & 1][1] = v_frag(ks_n, fb_n + 1 < kFB ? fb_n + 1 : fb_n);
                     }
-                }
-                if (fb0 == 0) {
-                    // Row sums of exactly the fp16 P the P.V MFMAs use.
 #pragma unroll
-                    for (int b = 0; b < 2; ++b) {
-                        st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph[b][ks], st.l[b], 0, 0, 0);
-                        if constexpr (kPrecise)
-                            st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pl[b][ks], st.l[b], 0, 0, 0);
+                    for (int h = 0; h < 2; ++h) {
+                        if (fb0 + h >= kFB) continue;
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) {
+                            st.o[b][fb0 + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[stage & 1][h], ph[b][ks], st.o[b][fb0 + h], 0, 0, 0);
+                            if constexpr (kPrecise)
+                                st.o[b][fb0 + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[stage & 1][h], pl[b][ks], st.o[b][fb0 + h], 0, 0, 0);
+                        }
                     }
+                    if (fb0 == 0) {
+                        // Row sums of exactly the fp16 P the P.V MFMAs use.
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) {
+                            st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph[b][ks], st.l[b], 0, 0, 0);
+                            if constexpr (kPrecise)
+                                st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pl[b][ks], st.l[b], 0, 0, 0);
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-                __builtin_amdgcn_sched_barrier(0);
             }
         }
         j = j_next;
