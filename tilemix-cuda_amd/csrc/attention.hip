@@ -22,10 +22,12 @@
 //    probabilities P.V uses, over all of the row's keys, on the matrix core
 //    instead of the VALU.
 //  * K, K8 and V tiles move HBM -> LDS with buffer_load ... lds (no VGPR
-//    staging): per-lane offsets into the padded LDS rows are computed once, each tile only changes a scalar offset, and rows past
-//    the end of the head read as zero. The V tile is fetched while the
-//    scores are computed and the next K tile while softmax and P.V run, with
-//    two barriers per tile and 44 KiB of LDS so two workgroups share a CU.
+//    staging): per-lane offsets into the padded LDS rows are computed once,
+//    each tile only changes a scalar offset, and rows past the end of the
+//    head read as zero. The V tile is fetched while the scores are computed
+//    and the next K tile while softmax and P.V run, with two barriers per
+//    tile; 44 KiB of tile buffers plus 18 KiB of quantized Q rows let two
+//    workgroups share a CU.
 //  * A 16x32 routing cell covers whole 16x16 MFMA blocks, so each route is
 //    uniform per MFMA and the branch is taken on wave-uniform route masks.
 //  * The optional in-kernel Q quantization reproduces quantize_tilemix_qk's
