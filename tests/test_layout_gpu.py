@@ -4,7 +4,9 @@
 * row-strided [S, H, D] tensors (head stride D, row stride H * D) give the
   same O, Q8/K8 and scales as the contiguous [H, S, D] layout, bit for bit,
   on the vector (d % 16 == 0) and element-wise (odd d) paths;
-* tilemix_quantize_qk_strided equals the contiguous batched quantizer.
+* tilemix_quantize_qk_strided equals the contiguous batched quantizer;
+* a head whose K / V span more than 2 GiB (4 MiB row stride) takes the
+  element-wise path and gives the contiguous run's bits.
 """
 from __future__ import annotations
 
@@ -119,3 +121,38 @@ def test_strided_quantizer_equals_contiguous(tm, cuda, heads, M, N, d):
         outs.append([t.cpu() for t in (q8, k8, qs, ks)])
     for x, y in zip(*outs):
         assert torch.equal(x, y)
+
+
+def test_heads_past_2gib_take_the_elementwise_path(tm, cuda):
+    """K and V rows 4 MiB apart, so a head spans more than 2 GiB: the vector
+    path's 32-bit buffer offsets cannot address it, the launch takes the
+    element-wise path, and O, Q8/K8 and scales equal the contiguous run's."""
+    import torch
+
+    heads, S, d = 1, 1024, 64
+    stride = (1 << 21) + 64  # elements between consecutive rows
+    print(f"huge row stride S={S} d={d} stride={stride}", flush=True)
+    Q, K, V = _inputs(torch, heads, S, d, 99)
+    route = _routes(torch, heads, S, 2, 21)
+    ref = _run(tm, torch, Q, K, V, heads, S, d, tm.DTYPE_F32, "hsd", False, False, route)
+    k_big = torch.empty(S * stride, dtype=torch.float16, device="cuda")
+    v_big = torch.empty(S * stride, dtype=torch.float16, device="cuda")
+    k_big.as_strided((S, d), (stride, 1)).copy_(K[0])
+    v_big.as_strided((S, d), (stride, 1)).copy_(V[0])
+    O = torch.full((heads, S, d), float("nan"), device="cuda")
+    K8 = torch.zeros(heads, S, d, dtype=torch.int8, device="cuda")
+    ks = torch.zeros(heads, (S + 63) // 64, dtype=torch.int16, device="cuda")
+    Q8 = torch.zeros(heads, S, d, dtype=torch.int8, device="cuda")
+    qs = torch.zeros(heads, (S + 127) // 128, dtype=torch.int16, device="cuda")
+    args = tm.BatchedArgs(Q=Q, K=k_big, V=v_big, O=O, heads=heads, M=S, N=S, d=d, score_scale=d ** -0.5,
+                          quantize=1, route_words=route, key_tiles_per_group=2, K8=K8, k_scales=ks, Q8=Q8,
+                          q_scales=qs, k_row_stride=stride, v_row_stride=stride)
+    tm.check(tm.attention_batched(args), "attention")
+    torch.cuda.synchronize()
+    got = (O.cpu(), Q8.cpu(), qs.cpu(), K8.cpu(), ks.cpu())
+    del k_big, v_big
+    for name, x, y in zip(("O", "Q8", "q_scales", "K8", "k_scales"), ref, got):
+        if x.dtype.is_floating_point:
+            assert torch.equal(x.view(torch.int32), y.view(torch.int32)), name
+        else:
+            assert torch.equal(x, y), name
