@@ -157,6 +157,10 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     unsigned char* const lds_k = smem;
     unsigned char* const lds_v = smem + L::kKBytes;
     unsigned char* const lds_k8 = smem + L::kKBytes + L::kVBytes;
+    // LDS byte addresses of the tile buffers (M0 of the tile DMA), converted once.
+    const unsigned lds_k_address = lds_address_of(smem);
+    const unsigned lds_v_address = lds_k_address + L::kKBytes;
+    const unsigned lds_k8_address = lds_v_address + L::kVBytes;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -370,14 +374,14 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 #pragma unroll
                 for (int t = 0; t < L::kKPerWave; ++t) {
                     const int w = wave + kWavesPerGroup * t;
-                    if (w < L::kKLoads) load_to_lds(rsrc_k, lds_k + 1024 * w, off_k[t], k0 * k_row_bytes);
+                    if (w < L::kKLoads) load_to_lds(rsrc_k, lds_k_address + 1024 * w, off_k[t], k0 * k_row_bytes);
                 }
             }
             if (need8) {
 #pragma unroll
                 for (int t = 0; t < L::kK8PerWave; ++t) {
                     const int w = wave + kWavesPerGroup * t;
-                    if (w < L::kK8Loads) load_to_lds(rsrc_k8, lds_k8 + 1024 * w, off_k8[t], k0 * d);
+                    if (w < L::kK8Loads) load_to_lds(rsrc_k8, lds_k8_address + 1024 * w, off_k8[t], k0 * d);
                 }
             }
         } else {
@@ -403,7 +407,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 #pragma unroll
             for (int t = 0; t < L::kVPerWave; ++t) {
                 const int w = wave + kWavesPerGroup * t;
-                if (w < L::kVLoads) load_to_lds(rsrc_v, lds_v + 1024 * w, off_v[t], k0 * v_row_bytes);
+                if (w < L::kVLoads) load_to_lds(rsrc_v, lds_v_address + 1024 * w, off_v[t], k0 * v_row_bytes);
             }
         } else {
             for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {

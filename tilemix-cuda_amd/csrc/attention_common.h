@@ -133,15 +133,22 @@ __device__ __forceinline__ int4v make_rsrc(const void* base, int bytes) {
                  __builtin_amdgcn_readfirstlane(bytes), static_cast<int>(kBufferFlags)};
 }
 
-// 16 bytes per lane from buffer offset soffset + voffset into LDS at
-// lds_base + 16 * lane (lds_base is wave-uniform; M0 carries it). Issued as
-// inline assembly so that the compiler does not treat it as an LDS store: it
-// would otherwise wait for every outstanding tile load before any later LDS
-// read it cannot prove disjoint. The kernels order these loads themselves -
-// s_waitcnt vmcnt, then a workgroup barrier, before any read of the tile.
-__device__ __forceinline__ void load_to_lds(int4v rsrc, const unsigned char* lds_base, int voffset, int soffset) {
-    const unsigned lds_address = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(
-        reinterpret_cast<unsigned long long>((__attribute__((address_space(3))) const void*)(lds_base))));
+// LDS byte address of a workgroup-shared buffer, for M0 of an LDS DMA. The
+// cast from a generic pointer carries a null check (two scalar instructions),
+// so kernels convert each buffer's base once and add offsets to the result.
+__device__ __forceinline__ unsigned lds_address_of(const void* shared) {
+    return __builtin_amdgcn_readfirstlane(static_cast<unsigned>(
+        reinterpret_cast<unsigned long long>((__attribute__((address_space(3))) const void*)(shared))));
+}
+
+// 16 bytes per lane from buffer offset soffset + voffset into LDS at byte
+// address lds_address + 16 * lane (lds_address is wave-uniform; M0 carries
+// it). Issued as inline assembly so that the compiler does not treat it as an
+// LDS store: it would otherwise wait for every outstanding tile load before
+// any later LDS read it cannot prove disjoint. The kernels order these loads
+// themselves - s_waitcnt vmcnt, then a workgroup barrier, before any read of
+// the tile.
+__device__ __forceinline__ void load_to_lds(int4v rsrc, unsigned lds_address, int voffset, int soffset) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
                  : "s"(lds_address), "v"(voffset), "s"(rsrc), "s"(soffset)
