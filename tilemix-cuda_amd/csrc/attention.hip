@@ -24,7 +24,9 @@
 //  * K, K8 and V tiles move HBM -> LDS with buffer_load ... lds (no VGPR
 //    staging): per-lane offsets into the padded LDS rows are computed once,
 //    each tile only changes a scalar offset, and rows past the end of the
-//    head read as zero. The V tile is fetched while the scores are computed
+//    head read as zero. Every wave issues the same number of loads per
+//    buffer (spare slots read out of range into a 1 KiB landing area), so
+//    the issue code has no branches. The V tile is fetched while the scores are computed
 //    and the next K tile while softmax and P.V run, with two barriers per
 //    tile; 44 KiB of tile buffers plus 18 KiB of quantized Q rows let two
 //    workgroups share a CU.
@@ -154,6 +156,8 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     // Quantized Q rows (B operand of the INT8 MFMA), read on INT8 tiles only.
     __shared__ __attribute__((aligned(16))) unsigned char lds_q8[L::kQ8Bytes];
     __shared__ unsigned group_bits[kWavesPerGroup];
+    // Landing area of the spare DMA slots (written with zeros, never read).
+    __shared__ __attribute__((aligned(16))) unsigned char lds_spare[1024];
     unsigned char* const lds_k = smem;
     unsigned char* const lds_v = smem + L::kKBytes;
     unsigned char* const lds_k8 = smem + L::kKBytes + L::kVBytes;
@@ -354,17 +358,32 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     const int4v rsrc_k8 = make_rsrc(p.int8_operands ? K8h : p.K8,
                                     static_cast<int>(p.int8_operands ? static_cast<std::int64_t>(N) * d : 0));
     const int k_row_bytes = static_cast<int>(p.k_row * 2), v_row_bytes = static_cast<int>(p.v_row * 2);
+    // Each wave issues the same number of DMAs per tile buffer, so the issue
+    // code has no branches: slot t of a wave moves 1 KiB piece wave + 4t, and
+    // a slot past the buffer's last piece reads out of range (zeros, no
+    // memory traffic) into lds_spare.
+    const unsigned lds_spare_address = lds_address_of(lds_spare);
     int off_k[L::kKPerWave], off_v[L::kVPerWave], off_k8[L::kK8PerWave];
+    unsigned dst_k[L::kKPerWave], dst_v[L::kVPerWave], dst_k8[L::kK8PerWave];
     if constexpr (kVector) {
 #pragma unroll
-        for (int t = 0; t < L::kKPerWave; ++t)
-            off_k[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kKStride, 2 * d, k_row_bytes);
+        for (int t = 0; t < L::kKPerWave; ++t) {
+            const int w = wave + kWavesPerGroup * t;
+            off_k[t] = w < L::kKLoads ? lane_offset(w, lane, L::kKStride, 2 * d, k_row_bytes) : kOutOfRange;
+            dst_k[t] = w < L::kKLoads ? lds_k_address + 1024 * w : lds_spare_address;
+        }
 #pragma unroll
-        for (int t = 0; t < L::kVPerWave; ++t)
-            off_v[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kVStride, 2 * d, v_row_bytes);
+        for (int t = 0; t < L::kVPerWave; ++t) {
+            const int w = wave + kWavesPerGroup * t;
+            off_v[t] = w < L::kVLoads ? lane_offset(w, lane, L::kVStride, 2 * d, v_row_bytes) : kOutOfRange;
+            dst_v[t] = w < L::kVLoads ? lds_v_address + 1024 * w : lds_spare_address;
+        }
 #pragma unroll
-        for (int t = 0; t < L::kK8PerWave; ++t)
-            off_k8[t] = lane_offset(wave + kWavesPerGroup * t, lane, L::kK8Stride, d, d);
+        for (int t = 0; t < L::kK8PerWave; ++t) {
+            const int w = wave + kWavesPerGroup * t;
+            off_k8[t] = w < L::kK8Loads ? lane_offset(w, lane, L::kK8Stride, d, d) : kOutOfRange;
+            dst_k8[t] = w < L::kK8Loads ? lds_k8_address + 1024 * w : lds_spare_address;
+        }
     }
     // K (FP16 cells) and K8 (INT8 cells) of tile j.
     auto issue_k = [&](int j, bool need16, bool need8) {
@@ -372,17 +391,11 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         if constexpr (kVector) {
             if (need16) {
 #pragma unroll
-                for (int t = 0; t < L::kKPerWave; ++t) {
-                    const int w = wave + kWavesPerGroup * t;
-                    if (w < L::kKLoads) load_to_lds(rsrc_k, lds_k_address + 1024 * w, off_k[t], k0 * k_row_bytes);
-                }
+                for (int t = 0; t < L::kKPerWave; ++t) load_to_lds(rsrc_k, dst_k[t], off_k[t], k0 * k_row_bytes);
             }
             if (need8) {
 #pragma unroll
-                for (int t = 0; t < L::kK8PerWave; ++t) {
-                    const int w = wave + kWavesPerGroup * t;
-                    if (w < L::kK8Loads) load_to_lds(rsrc_k8, lds_k8_address + 1024 * w, off_k8[t], k0 * d);
-                }
+                for (int t = 0; t < L::kK8PerWave; ++t) load_to_lds(rsrc_k8, dst_k8[t], off_k8[t], k0 * d);
             }
         } else {
             if (need16) {
@@ -405,10 +418,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         const int k0 = j * kTileKeys;
         if constexpr (kVector) {
 #pragma unroll
-            for (int t = 0; t < L::kVPerWave; ++t) {
-                const int w = wave + kWavesPerGroup * t;
-                if (w < L::kVLoads) load_to_lds(rsrc_v, lds_v_address + 1024 * w, off_v[t], k0 * v_row_bytes);
-            }
+            for (int t = 0; t < L::kVPerWave; ++t) load_to_lds(rsrc_v, dst_v[t], off_v[t], k0 * v_row_bytes);
         } else {
             for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
                 const int row = e / kDP, f = e % kDP, key = k0 + row;
