@@ -30,6 +30,12 @@
 //    and the next K tile while softmax and P.V run, with two barriers per
 //    tile; 44 KiB of tile buffers plus 18 KiB of quantized Q rows let two
 //    workgroups share a CU.
+//  * Each SIMD runs one wave of each of the CU's two workgroups. A tile is an
+//    MFMA phase (P.V, barrier, next scores) and a VALU phase (softmax). A
+//    wave's issue priority is low in the first half of each phase and high
+//    in the second, so of two waves in the same phase the one further along
+//    wins arbitration and leaves it first: this pushes the pair apart, one
+//    on the matrix core while the other runs exponentials.
 //  * A 16x32 routing cell covers whole 16x16 MFMA blocks, so each route is
 //    uniform per MFMA and the branch is taken on wave-uniform route masks.
 //  * The optional in-kernel Q quantization reproduces quantize_tilemix_qk's
@@ -143,6 +149,7 @@ __device__ __forceinline__ void softmax_tile(RowState<kFB>& st, const float4v (&
                     pl[b][ks][4 + r] = static_cast<_Float16>(e - static_cast<float>(he));
                 }
             }
+        if (b == 0) set_priority<2>();  // second half of the VALU phase
     }
 }
 
@@ -494,6 +501,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         const int k0 = j * kTileKeys;
         const std::uint32_t int8_mask = cur_int8, skip_mask = cur_skip;
         tile_barrier();  // K_j landed; every wave finished P.V of the previous tile
+        set_priority<2>();  // second half of the MFMA phase (P.V, then these scores)
         issue_v(j);
 
         const unsigned wave_int8 = (int8_mask >> (4 * wave)) & 0xfu;
@@ -671,6 +679,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         }
 
         tile_barrier();  // V_j landed; every wave finished reading K_j
+        set_priority<0>();  // first half of the VALU phase
         const int j_next = next_tile(j + 1);
         if (j_next < tiles) issue_k(j_next, needs16(cur_int8, cur_skip), cur_int8 != 0);
 
@@ -686,6 +695,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                     return concat(read_tr16(v_lo + 32 * fb), read_tr16(v_lo + 16 * L::kVStride + 32 * fb));
                 };
                 constexpr int kPairs = kFB;  // (ks, fb pair) stages: 2 * kFB / 2
+                set_priority<0>();  // first half of the MFMA phase
                 half8 vf[2][2];
                 vf[0][0] = v_frag(0, 0);
                 vf[0][1] = v_frag(0, kFB > 1 ? 1 : 0);

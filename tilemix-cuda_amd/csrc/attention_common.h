@@ -232,6 +232,16 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Issue priority of this wave against the other waves of its SIMD, set at
+// this point of the instruction stream (the compiler moves nothing across).
+template <int kLevel>
+__device__ __forceinline__ void set_priority() {
+    static_assert(kLevel >= 0 && kLevel <= 3, "s_setprio range");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(kLevel);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // Workgroup index -> (head, row group). Workgroups are dealt round-robin to
 // the XCDs; all row groups of a head run on one XCD so that its K / V / K8
 // stay in that XCD's L2. Causal problems start the heaviest (last) row
