@@ -551,7 +551,6 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                     __builtin_amdgcn_sched_barrier(0);
                 }
             };
-            auto load_q8 = [&]() {};
             // Exact int32 dots of key block kb for both query blocks.
             auto int8_dots = [&](int kb, int4v& acc0, int4v& acc1) {
                 acc0 = int4v{0, 0, 0, 0};
@@ -580,7 +579,6 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 fp16_scores();
                 c = p.score_log2;
             } else if (wave_skip == 0 && wave_int8 == 0xfu) {
-                load_q8();
                 int4v acc[2][4];
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
@@ -632,7 +630,6 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                         for (int kb = 0; kb < 4; ++kb) s[b][kb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
                 }
                 if (wave_int8) {
-                    load_q8();
 #pragma unroll
                     for (int kb = 0; kb < 4; ++kb) {
                         int4v acc[2];
