@@ -194,6 +194,8 @@ BATCH_CASES = [
     (1, 4096, 4096, 128, 2, True, 0.0),
     (2, 77, 333, 128, 1, True, 0.3),   # causal with fewer queries than keys
     (2, 500, 130, 64, 2, True, 0.0),   # causal with more queries than keys
+    (2, 200, 333, 112, 2, True, 0.2),  # d > 96 with the last 16-byte chunks of each row absent
+    (2, 150, 270, 100, 1, False, 0.0), # d > 96 on the element-wise path (d % 16 != 0)
 ]
 
 

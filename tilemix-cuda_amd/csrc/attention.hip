@@ -22,13 +22,14 @@
 //    probabilities P.V uses, over all of the row's keys, on the matrix core
 //    instead of the VALU.
 //  * K, K8 and V tiles move HBM -> LDS with buffer_load ... lds (no VGPR
-//    staging): per-lane offsets into the padded LDS rows are computed once,
-//    each tile only changes a scalar offset, and rows past the end of the
-//    head read as zero. Every wave issues the same number of loads per
-//    buffer (spare slots read out of range into a 1 KiB landing area), so
-//    the issue code has no branches. The V tile is fetched while the scores are computed
+//    staging): per-lane offsets into the LDS rows (padded, or for d > 96
+//    unpadded with rotated 16-byte chunks) are computed once, each tile only
+//    changes a scalar offset, and rows past the end of the head read as
+//    zero. Every wave issues the same number of loads per buffer (spare
+//    slots read out of range into a 1 KiB landing area), so the issue code
+//    has no branches. The V tile is fetched while the scores are computed
 //    and the next K tile while softmax and P.V run, with two barriers per
-//    tile; 44 KiB of tile buffers plus 18 KiB of quantized Q rows let two
+//    tile; 41 KiB of tile buffers plus 18 KiB of quantized Q rows let two
 //    workgroups share a CU.
 //  * Each SIMD runs one wave of each of the CU's two workgroups. A tile is an
 //    MFMA phase (P.V, barrier, next scores) and a VALU phase (softmax). A
@@ -67,12 +68,16 @@ struct Layout {
     static constexpr int kD8C = (DC + 1) / 2;      // 64-feature chunks, int8 path
     static constexpr int kDP8 = 64 * kD8C;
     static constexpr int kFB = kDP / 16;           // 16-feature output blocks
-    // Row strides pad each row by 16 (K, K8) or 32 (V) bytes. The transposed
-    // V reads are then free of bank conflicts; the K / K8 fragment reads see
-    // two-way conflicts, which measured cheaper than a 32-byte pad (more DMA
-    // lanes per tile).
-    static constexpr int kKStride = kDP * 2 + 16;
-    static constexpr int kVStride = kDP * 2 + 32;
+    // d <= 96: row strides pad each row by 16 (K, K8) or 32 (V) bytes. The
+    // transposed V reads are then free of bank conflicts; the K / K8 fragment
+    // reads see two-way conflicts, which measured cheaper than a 32-byte pad
+    // (more DMA lanes per tile). d > 96 (kRotate): K and V rows are 256 bytes,
+    // unpadded, and 16-byte chunk c of row r sits at chunk position
+    // (c + 2r) mod 16 - the bank pattern of a 32-byte pad (conflict-free K
+    // and V^T reads) without pad bytes to move.
+    static constexpr bool kRotate = DC == 4;
+    static constexpr int kKStride = kRotate ? 256 : kDP * 2 + 16;
+    static constexpr int kVStride = kRotate ? 256 : kDP * 2 + 32;
     static constexpr int kK8Stride = kDP8 + 16;
     static constexpr int kKBytes = kTileKeys * kKStride;
     static constexpr int kVBytes = kTileKeys * kVStride;
@@ -89,6 +94,27 @@ struct Layout {
     static constexpr int kSmemBytes = kKBytes + kVBytes + kK8Bytes;
     static_assert(kKBytes % 1024 == 0 && kVBytes % 1024 == 0 && kK8Bytes % 1024 == 0,
                   "tiles are whole wave loads");
+    // Offset of byte `byte` (< 2 * kDP) of row `row` in the K / V tile.
+    __device__ static int k_at(int row, int byte) {
+        if constexpr (kRotate) return row * 256 + ((((byte >> 4) + 2 * row) & 15) << 4) + (byte & 15);
+        else return row * kKStride + byte;
+    }
+    __device__ static int v_at(int row, int byte) {
+        if constexpr (kRotate) return row * 256 + ((((byte >> 4) + 2 * row) & 15) << 4) + (byte & 15);
+        else return row * kVStride + byte;
+    }
+    // Global offset that DMA lane `lane` of 1 KiB piece w fetches (kOutOfRange
+    // past the row's bytes): the inverse of k_at / v_at.
+    __device__ static int kv_lane_offset(int w, int lane, int stride, int row_bytes, int global_row_bytes) {
+        if constexpr (kRotate) {
+            const int landing = 1024 * w + 16 * lane;
+            const int row = landing >> 8;
+            const int column = ((((landing >> 4) & 15) - 2 * row) & 15) << 4;
+            return column < row_bytes ? row * global_row_bytes + column : kOutOfRange;
+        } else {
+            return lane_offset(w, lane, stride, row_bytes, global_row_bytes);
+        }
+    }
 };
 
 // Online-softmax state of the two 16-row query blocks a wave owns (scores in
@@ -376,13 +402,13 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 #pragma unroll
         for (int t = 0; t < L::kKPerWave; ++t) {
             const int w = wave + kWavesPerGroup * t;
-            off_k[t] = w < L::kKLoads ? lane_offset(w, lane, L::kKStride, 2 * d, k_row_bytes) : kOutOfRange;
+            off_k[t] = w < L::kKLoads ? L::kv_lane_offset(w, lane, L::kKStride, 2 * d, k_row_bytes) : kOutOfRange;
             dst_k[t] = w < L::kKLoads ? lds_k_address + 1024 * w : lds_spare_address;
         }
 #pragma unroll
         for (int t = 0; t < L::kVPerWave; ++t) {
             const int w = wave + kWavesPerGroup * t;
-            off_v[t] = w < L::kVLoads ? lane_offset(w, lane, L::kVStride, 2 * d, v_row_bytes) : kOutOfRange;
+            off_v[t] = w < L::kVLoads ? L::kv_lane_offset(w, lane, L::kVStride, 2 * d, v_row_bytes) : kOutOfRange;
             dst_v[t] = w < L::kVLoads ? lds_v_address + 1024 * w : lds_spare_address;
         }
 #pragma unroll
@@ -408,7 +434,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             if (need16) {
                 for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
                     const int row = e / kDP, f = e % kDP, key = k0 + row;
-                    *reinterpret_cast<std::uint16_t*>(lds_k + row * L::kKStride + 2 * f) =
+                    *reinterpret_cast<std::uint16_t*>(lds_k + L::k_at(row, 2 * f)) =
                         (key < N && f < d) ? Kh[static_cast<std::int64_t>(key) * p.k_row + f] : 0;
                 }
             }
@@ -429,7 +455,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         } else {
             for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
                 const int row = e / kDP, f = e % kDP, key = k0 + row;
-                *reinterpret_cast<std::uint16_t*>(lds_v + row * L::kVStride + 2 * f) =
+                *reinterpret_cast<std::uint16_t*>(lds_v + L::v_at(row, 2 * f)) =
                     (key < N && f < d) ? Vh[static_cast<std::int64_t>(key) * p.v_row + f] : 0;
             }
         }
@@ -450,6 +476,14 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 q8f[b][m] = *reinterpret_cast<const int4v*>(
                     lds_q8 + (wave * kRowsPerWave + 16 * b + i) * L::kQ8Stride + 64 * m + 16 * g);
     }
+    // Per-lane LDS offsets of the K fragment (feature chunk dc, key block 0)
+    // and V^T fragment (feature block fb, key step 0) reads; key blocks and
+    // steps add whole rows (multiples of 16, which keep the chunk rotation).
+    int k_lane[DC], v_lane[kFB];
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc) k_lane[dc] = L::k_at(i, (32 * dc + 8 * g) * 2);
+#pragma unroll
+    for (int fb = 0; fb < kFB; ++fb) v_lane[fb] = L::v_at(4 * g + (i >> 2), 8 * (i & 3) + 32 * fb);
     // ---------------------------------------------------------- key loop
     RowState<kFB> st;
 #pragma unroll
@@ -536,8 +570,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 auto load_dc = [&](int dc, half8 (&dst)[4]) {
 #pragma unroll
                     for (int kb = 0; kb < 4; ++kb)
-                        dst[kb] = *reinterpret_cast<const half8*>(
-                            lds_k + (16 * kb + i) * L::kKStride + (32 * dc + 8 * g) * 2);
+                        dst[kb] = *reinterpret_cast<const half8*>(lds_k + 16 * L::kKStride * kb + k_lane[dc]);
                 };
                 load_dc(0, kf[0]);
 #pragma unroll
@@ -688,8 +721,8 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 // V^T fragments two 16-feature blocks at a time, the next pair
                 // read while this pair's MFMAs issue.
                 auto v_frag = [&](int ks, int fb) {
-                    const unsigned char* v_lo = lds_v + (32 * ks + 4 * g + (i >> 2)) * L::kVStride + 8 * (i & 3);
-                    return concat(read_tr16(v_lo + 32 * fb), read_tr16(v_lo + 16 * L::kVStride + 32 * fb));
+                    const unsigned char* v_lo = lds_v + 32 * L::kVStride * ks + v_lane[fb];
+                    return concat(read_tr16(v_lo), read_tr16(v_lo + 16 * L::kVStride));
                 };
                 constexpr int kPairs = kFB;  // (ks, fb pair) stages: 2 * kFB / 2
                 set_priority<0>();  // first half of the MFMA phase
