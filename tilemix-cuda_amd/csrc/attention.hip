@@ -179,6 +179,29 @@ __device__ __forceinline__ void softmax_tile(RowState<kFB>& st, const float4v (&
     }
 }
 
+// load_to_lds with M0 = lds_address + kOffset, the add issued inside the asm
+// so that the compiler keeps one scalar address per buffer, not one per slot.
+template <int kOffset>
+__device__ __forceinline__ void load_to_lds_at(int4v rsrc, unsigned lds_address, int voffset, int soffset) {
+    if constexpr (kOffset == 0) {
+        load_to_lds(rsrc, lds_address, voffset, soffset);
+    } else {
+        asm volatile("s_add_u32 m0, %0, %4\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                     :
+                     : "s"(lds_address), "v"(voffset), "s"(rsrc), "s"(soffset), "i"(kOffset)
+                     : "memory");
+    }
+}
+
+// The four 1 KiB pieces of a 16 KiB tile buffer one wave moves: slot t lands
+// 4 KiB past slot t - 1 (pieces wave, wave + 4, wave + 8, wave + 12).
+__device__ __forceinline__ void load_four_slots(int4v rsrc, unsigned first, const int (&voffset)[4], int soffset) {
+    load_to_lds_at<0>(rsrc, first, voffset[0], soffset);
+    load_to_lds_at<4096>(rsrc, first, voffset[1], soffset);
+    load_to_lds_at<8192>(rsrc, first, voffset[2], soffset);
+    load_to_lds_at<12288>(rsrc, first, voffset[3], soffset);
+}
+
 template <int DC, bool kVector, bool kPrecise, bool kDots>
 __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kernel(const AttnParams p) {
     using L = Layout<DC>;
@@ -423,8 +446,12 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         const int k0 = j * kTileKeys;
         if constexpr (kVector) {
             if (need16) {
+                if constexpr (L::kKLoads == 4 * kWavesPerGroup) {
+                    load_four_slots(rsrc_k, dst_k[0], off_k, k0 * k_row_bytes);
+                } else {
 #pragma unroll
-                for (int t = 0; t < L::kKPerWave; ++t) load_to_lds(rsrc_k, dst_k[t], off_k[t], k0 * k_row_bytes);
+                    for (int t = 0; t < L::kKPerWave; ++t) load_to_lds(rsrc_k, dst_k[t], off_k[t], k0 * k_row_bytes);
+                }
             }
             if (need8) {
 #pragma unroll
@@ -450,8 +477,12 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     auto issue_v = [&](int j) {
         const int k0 = j * kTileKeys;
         if constexpr (kVector) {
+            if constexpr (L::kVLoads == 4 * kWavesPerGroup) {
+                load_four_slots(rsrc_v, dst_v[0], off_v, k0 * v_row_bytes);
+            } else {
 #pragma unroll
-            for (int t = 0; t < L::kVPerWave; ++t) load_to_lds(rsrc_v, dst_v[t], off_v[t], k0 * v_row_bytes);
+                for (int t = 0; t < L::kVPerWave; ++t) load_to_lds(rsrc_v, dst_v[t], off_v[t], k0 * v_row_bytes);
+            }
         } else {
             for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
                 const int row = e / kDP, f = e % kDP, key = k0 + row;
