@@ -29,7 +29,7 @@
 //    slots read out of range into a 1 KiB landing area), so the issue code
 //    has no branches. The V tile is fetched while the scores are computed
 //    and the next K tile while softmax and P.V run, with two barriers per
-//    tile; 41 KiB of tile buffers plus 18 KiB of quantized Q rows let two
+//    tile; 40 KiB of tile buffers plus 18 KiB of quantized Q rows let two
 //    workgroups share a CU.
 //  * Each SIMD runs one wave of each of the CU's two workgroups. A tile is an
 //    MFMA phase (P.V, barrier, next scores) and a VALU phase (softmax). A
@@ -78,7 +78,9 @@ struct Layout {
     static constexpr bool kRotate = DC == 4;
     static constexpr int kKStride = kRotate ? 256 : kDP * 2 + 16;
     static constexpr int kVStride = kRotate ? 256 : kDP * 2 + 32;
-    static constexpr int kK8Stride = kDP8 + 16;
+    // K8 rows (d > 96: 128 bytes, unpadded): chunk c of row r at chunk
+    // position (c + (r & 6)) mod 8.
+    static constexpr int kK8Stride = kRotate ? kDP8 : kDP8 + 16;
     static constexpr int kKBytes = kTileKeys * kKStride;
     static constexpr int kVBytes = kTileKeys * kVStride;
     static constexpr int kK8Bytes = kTileKeys * kK8Stride;
@@ -102,6 +104,20 @@ struct Layout {
     __device__ static int v_at(int row, int byte) {
         if constexpr (kRotate) return row * 256 + ((((byte >> 4) + 2 * row) & 15) << 4) + (byte & 15);
         else return row * kVStride + byte;
+    }
+    __device__ static int k8_at(int row, int byte) {
+        if constexpr (kRotate) return row * kDP8 + ((((byte >> 4) + (row & 6)) & 7) << 4) + (byte & 15);
+        else return row * kK8Stride + byte;
+    }
+    __device__ static int k8_lane_offset(int w, int lane, int row_bytes) {
+        if constexpr (kRotate) {
+            const int landing = 1024 * w + 16 * lane;
+            const int row = landing / kDP8;
+            const int column = ((((landing >> 4) & 7) - (row & 6)) & 7) << 4;
+            return column < row_bytes ? row * row_bytes + column : kOutOfRange;
+        } else {
+            return lane_offset(w, lane, kK8Stride, row_bytes, row_bytes);
+        }
     }
     // Global offset that DMA lane `lane` of 1 KiB piece w fetches (kOutOfRange
     // past the row's bytes): the inverse of k_at / v_at.
@@ -437,7 +453,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 #pragma unroll
         for (int t = 0; t < L::kK8PerWave; ++t) {
             const int w = wave + kWavesPerGroup * t;
-            off_k8[t] = w < L::kK8Loads ? lane_offset(w, lane, L::kK8Stride, d, d) : kOutOfRange;
+            off_k8[t] = w < L::kK8Loads ? L::k8_lane_offset(w, lane, d) : kOutOfRange;
             dst_k8[t] = w < L::kK8Loads ? lds_k8_address + 1024 * w : lds_spare_address;
         }
     }
@@ -468,7 +484,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             if (need8) {
                 for (int e = tid; e < kTileKeys * L::kDP8; e += kThreadsPerGroup) {
                     const int row = e / L::kDP8, f = e % L::kDP8, key = k0 + row;
-                    lds_k8[row * L::kK8Stride + f] =
+                    lds_k8[L::k8_at(row, f)] =
                         (key < N && f < d) ? static_cast<unsigned char>(K8h[static_cast<std::int64_t>(key) * d + f]) : 0;
                 }
             }
@@ -510,7 +526,9 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     // Per-lane LDS offsets of the K fragment (feature chunk dc, key block 0)
     // and V^T fragment (feature block fb, key step 0) reads; key blocks and
     // steps add whole rows (multiples of 16, which keep the chunk rotation).
-    int k_lane[DC], v_lane[kFB];
+    int k_lane[DC], v_lane[kFB], k8_lane[kD8C];
+#pragma unroll
+    for (int m = 0; m < kD8C; ++m) k8_lane[m] = L::k8_at(i, 64 * m + 16 * g);
 #pragma unroll
     for (int dc = 0; dc < DC; ++dc) k_lane[dc] = L::k_at(i, (32 * dc + 8 * g) * 2);
 #pragma unroll
@@ -622,7 +640,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 #pragma unroll
                 for (int m = 0; m < kD8C; ++m) {
                     const int4v kf = *reinterpret_cast<const int4v*>(
-                        lds_k8 + (16 * kb + i) * L::kK8Stride + 64 * m + 16 * g);
+                        lds_k8 + 16 * L::kK8Stride * kb + k8_lane[m]);
                     acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, q8f[0][m], acc0, 0, 0, 0);
                     acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, q8f[1][m], acc1, 0, 0, 0);
                 }
@@ -652,7 +670,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 auto load_m = [&](int m, int4v (&dst)[4]) {
 #pragma unroll
                     for (int kb = 0; kb < 4; ++kb)
-                        dst[kb] = *reinterpret_cast<const int4v*>(lds_k8 + (16 * kb + i) * L::kK8Stride + 64 * m + 16 * g);
+                        dst[kb] = *reinterpret_cast<const int4v*>(lds_k8 + 16 * L::kK8Stride * kb + k8_lane[m]);
                 };
                 load_m(0, kf8[0]);
 #pragma unroll
