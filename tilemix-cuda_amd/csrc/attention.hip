@@ -22,8 +22,9 @@
 //    probabilities P.V uses, over all of the row's keys, on the matrix core
 //    instead of the VALU.
 //  * K, K8 and V tiles move HBM -> LDS with buffer_load ... lds (no VGPR
-//    staging): per-lane offsets into the LDS rows (padded, or for d > 96
-//    unpadded with rotated 16-byte chunks) are computed once, each tile only
+//    staging): per-lane offsets into the LDS rows (unpadded with rotated
+//    16-byte chunks where rows are 128 or 256 bytes, else padded) are
+//    computed once, each tile only
 //    changes a scalar offset, and rows past the end of the head read as
 //    zero. Every wave issues the same number of loads per buffer (spare
 //    slots read out of range into a 1 KiB landing area), so the issue code
@@ -68,19 +69,20 @@ struct Layout {
     static constexpr int kD8C = (DC + 1) / 2;      // 64-feature chunks, int8 path
     static constexpr int kDP8 = 64 * kD8C;
     static constexpr int kFB = kDP / 16;           // 16-feature output blocks
-    // d <= 96: row strides pad each row by 16 (K, K8) or 32 (V) bytes. The
-    // transposed V reads are then free of bank conflicts; the K / K8 fragment
-    // reads see two-way conflicts, which measured cheaper than a 32-byte pad
-    // (more DMA lanes per tile). d > 96 (kRotate): K and V rows are 256 bytes,
-    // unpadded, and 16-byte chunk c of row r sits at chunk position
-    // (c + 2r) mod 16 - the bank pattern of a 32-byte pad (conflict-free K
-    // and V^T reads) without pad bytes to move.
-    static constexpr bool kRotate = DC == 4;
-    static constexpr int kKStride = kRotate ? 256 : kDP * 2 + 16;
-    static constexpr int kVStride = kRotate ? 256 : kDP * 2 + 32;
-    // K8 rows (d > 96: 128 bytes, unpadded): chunk c of row r at chunk
-    // position (c + (r & 6)) mod 8.
-    static constexpr int kK8Stride = kRotate ? kDP8 : kDP8 + 16;
+    // K / V rows hold 2 * kDP bytes. Rows of 256 bytes (d > 96) and 128 bytes
+    // (32 < d <= 64) are unpadded, with 16-byte chunk c of row r at chunk
+    // position (c + rot(r)) mod (chunks per row), rot(r) = 2r mod 16 on
+    // 256-byte rows and r & 6 on 128-byte rows: the bank pattern of a 32-byte
+    // pad, under which the K fragment and transposed V reads are
+    // conflict-free, with no pad bytes to move. Other rows are padded by 16 (K)
+    // or 32 (V) bytes. K8 rows of 128 bytes (d > 64) take the r & 6 rotation,
+    // shorter ones a 16-byte pad.
+    static constexpr int kRowBytes = kDP * 2;
+    static constexpr bool kRotate = kRowBytes == 256 || kRowBytes == 128;
+    static constexpr bool kRotate8 = kDP8 == 128;
+    static constexpr int kKStride = kRotate ? kRowBytes : kRowBytes + 16;
+    static constexpr int kVStride = kRotate ? kRowBytes : kRowBytes + 32;
+    static constexpr int kK8Stride = kRotate8 ? kDP8 : kDP8 + 16;
     static constexpr int kKBytes = kTileKeys * kKStride;
     static constexpr int kVBytes = kTileKeys * kVStride;
     static constexpr int kK8Bytes = kTileKeys * kK8Stride;
@@ -96,40 +98,48 @@ struct Layout {
     static constexpr int kSmemBytes = kKBytes + kVBytes + kK8Bytes;
     static_assert(kKBytes % 1024 == 0 && kVBytes % 1024 == 0 && kK8Bytes % 1024 == 0,
                   "tiles are whole wave loads");
-    // Offset of byte `byte` (< 2 * kDP) of row `row` in the K / V tile.
+    // Chunk rotation of a rotated row of kChunks 16-byte chunks.
+    template <int kChunks>
+    __device__ static int rot(int row) {
+        static_assert(kChunks == 16 || kChunks == 8, "rotated rows are 256 or 128 bytes");
+        return kChunks == 16 ? (2 * row) & 15 : row & 6;
+    }
+    // Offset of byte `byte` of row `row` in a rotated tile.
+    template <int kChunks>
+    __device__ static int rotated(int row, int byte) {
+        return row * 16 * kChunks + ((((byte >> 4) + rot<kChunks>(row)) & (kChunks - 1)) << 4) + (byte & 15);
+    }
+    // Global offset that DMA lane `lane` of 1 KiB piece w fetches for a
+    // rotated tile (kOutOfRange past the row's bytes): the inverse of rotated.
+    template <int kChunks>
+    __device__ static int rotated_lane(int w, int lane, int row_bytes, int global_row_bytes) {
+        const int landing = 1024 * w + 16 * lane;
+        const int row = landing / (16 * kChunks);
+        const int column = ((((landing >> 4) & (kChunks - 1)) - rot<kChunks>(row)) & (kChunks - 1)) << 4;
+        return column < row_bytes ? row * global_row_bytes + column : kOutOfRange;
+    }
+    // Offset of byte `byte` (< 2 * kDP, or < kDP8 for K8) of row `row` in the
+    // K / V / K8 tile.
     __device__ static int k_at(int row, int byte) {
-        if constexpr (kRotate) return row * 256 + ((((byte >> 4) + 2 * row) & 15) << 4) + (byte & 15);
+        if constexpr (kRotate) return rotated<kRowBytes / 16>(row, byte);
         else return row * kKStride + byte;
     }
     __device__ static int v_at(int row, int byte) {
-        if constexpr (kRotate) return row * 256 + ((((byte >> 4) + 2 * row) & 15) << 4) + (byte & 15);
+        if constexpr (kRotate) return rotated<kRowBytes / 16>(row, byte);
         else return row * kVStride + byte;
     }
     __device__ static int k8_at(int row, int byte) {
-        if constexpr (kRotate) return row * kDP8 + ((((byte >> 4) + (row & 6)) & 7) << 4) + (byte & 15);
+        if constexpr (kRotate8) return rotated<8>(row, byte);
         else return row * kK8Stride + byte;
     }
-    __device__ static int k8_lane_offset(int w, int lane, int row_bytes) {
-        if constexpr (kRotate) {
-            const int landing = 1024 * w + 16 * lane;
-            const int row = landing / kDP8;
-            const int column = ((((landing >> 4) & 7) - (row & 6)) & 7) << 4;
-            return column < row_bytes ? row * row_bytes + column : kOutOfRange;
-        } else {
-            return lane_offset(w, lane, kK8Stride, row_bytes, row_bytes);
-        }
-    }
-    // Global offset that DMA lane `lane` of 1 KiB piece w fetches (kOutOfRange
-    // past the row's bytes): the inverse of k_at / v_at.
+    // Global offset that DMA lane `lane` of 1 KiB piece w fetches.
     __device__ static int kv_lane_offset(int w, int lane, int stride, int row_bytes, int global_row_bytes) {
-        if constexpr (kRotate) {
-            const int landing = 1024 * w + 16 * lane;
-            const int row = landing >> 8;
-            const int column = ((((landing >> 4) & 15) - 2 * row) & 15) << 4;
-            return column < row_bytes ? row * global_row_bytes + column : kOutOfRange;
-        } else {
-            return lane_offset(w, lane, stride, row_bytes, global_row_bytes);
-        }
+        if constexpr (kRotate) return rotated_lane<kRowBytes / 16>(w, lane, row_bytes, global_row_bytes);
+        else return lane_offset(w, lane, stride, row_bytes, global_row_bytes);
+    }
+    __device__ static int k8_lane_offset(int w, int lane, int row_bytes) {
+        if constexpr (kRotate8) return rotated_lane<8>(w, lane, row_bytes, row_bytes);
+        else return lane_offset(w, lane, kK8Stride, row_bytes, row_bytes);
     }
 };
 
