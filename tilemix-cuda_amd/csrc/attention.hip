@@ -24,14 +24,13 @@
 //  * K, K8 and V tiles move HBM -> LDS with buffer_load ... lds (no VGPR
 //    staging): per-lane offsets into the LDS rows (unpadded with rotated
 //    16-byte chunks where rows are 128 or 256 bytes, else padded) are
-//    computed once, each tile only
-//    changes a scalar offset, and rows past the end of the head read as
-//    zero. Every wave issues the same number of loads per buffer (spare
-//    slots read out of range into a 1 KiB landing area), so the issue code
-//    has no branches. The V tile is fetched while the scores are computed
-//    and the next K tile while softmax and P.V run, with two barriers per
-//    tile; 40 KiB of tile buffers plus 18 KiB of quantized Q rows let two
-//    workgroups share a CU.
+//    computed once, each tile only changes a scalar offset, and rows past
+//    the end of the head read as zero. Every wave issues the same number of
+//    loads per buffer (spare slots read out of range into a 1 KiB landing
+//    area), so the issue code has no branches. The V tile is fetched while
+//    the scores are computed and the next K tile while softmax and P.V run,
+//    with two barriers per tile; at d = 128, 40 KiB of tile buffers plus
+//    18 KiB of quantized Q rows let two workgroups share a CU.
 //  * Each SIMD runs one wave of each of the CU's two workgroups. A tile is an
 //    MFMA phase (P.V, barrier, next scores) and a VALU phase (softmax). A
 //    wave's issue priority is low in the first half of each phase and high
