@@ -23,7 +23,7 @@
 //    instead of the VALU.
 //  * K, K8 and V tiles move HBM -> LDS with buffer_load ... lds (no VGPR
 //    staging): per-lane offsets into the LDS rows (unpadded with rotated
-//    16-byte chunks where rows are 128 or 256 bytes, else padded) are
+//    16-byte chunks: all K8 rows, K / V rows of 128 or 256 bytes) are
 //    computed once, each tile only changes a scalar offset, and rows past
 //    the end of the head read as zero. Every wave issues the same number of
 //    loads per buffer (spare slots read out of range into a 1 KiB landing
@@ -74,11 +74,11 @@ struct Layout {
     // 256-byte rows and r & 6 on 128-byte rows: the bank pattern of a 32-byte
     // pad, under which the K fragment and transposed V reads are
     // conflict-free, with no pad bytes to move. Other rows are padded by 16 (K)
-    // or 32 (V) bytes. K8 rows of 128 bytes (d > 64) take the r & 6 rotation,
-    // shorter ones a 16-byte pad.
+    // or 32 (V) bytes. K8 rows are 128 bytes (d > 64, r & 6 rotation) or 64
+    // bytes (2 * ((r >> 2) & 1), mod 4).
     static constexpr int kRowBytes = kDP * 2;
     static constexpr bool kRotate = kRowBytes == 256 || kRowBytes == 128;
-    static constexpr bool kRotate8 = kDP8 == 128;
+    static constexpr bool kRotate8 = kDP8 == 128 || kDP8 == 64;
     static constexpr int kKStride = kRotate ? kRowBytes : kRowBytes + 16;
     static constexpr int kVStride = kRotate ? kRowBytes : kRowBytes + 32;
     static constexpr int kK8Stride = kRotate8 ? kDP8 : kDP8 + 16;
@@ -100,8 +100,8 @@ struct Layout {
     // Chunk rotation of a rotated row of kChunks 16-byte chunks.
     template <int kChunks>
     __device__ static int rot(int row) {
-        static_assert(kChunks == 16 || kChunks == 8, "rotated rows are 256 or 128 bytes");
-        return kChunks == 16 ? (2 * row) & 15 : row & 6;
+        static_assert(kChunks == 16 || kChunks == 8 || kChunks == 4, "rotated rows are 256, 128 or 64 bytes");
+        return kChunks == 16 ? (2 * row) & 15 : kChunks == 8 ? row & 6 : 2 * ((row >> 2) & 1);
     }
     // Offset of byte `byte` of row `row` in a rotated tile.
     template <int kChunks>
@@ -128,7 +128,7 @@ struct Layout {
         else return row * kVStride + byte;
     }
     __device__ static int k8_at(int row, int byte) {
-        if constexpr (kRotate8) return rotated<8>(row, byte);
+        if constexpr (kRotate8) return rotated<kDP8 / 16>(row, byte);
         else return row * kK8Stride + byte;
     }
     // Global offset that DMA lane `lane` of 1 KiB piece w fetches.
@@ -137,7 +137,7 @@ struct Layout {
         else return lane_offset(w, lane, stride, row_bytes, global_row_bytes);
     }
     __device__ static int k8_lane_offset(int w, int lane, int row_bytes) {
-        if constexpr (kRotate8) return rotated_lane<8>(w, lane, row_bytes, row_bytes);
+        if constexpr (kRotate8) return rotated_lane<kDP8 / 16>(w, lane, row_bytes, row_bytes);
         else return lane_offset(w, lane, kK8Stride, row_bytes, row_bytes);
     }
 };
