@@ -218,13 +218,19 @@ __device__ __forceinline__ void load_to_lds_at(int4v rsrc, unsigned lds_address,
     }
 }
 
-// The four 1 KiB pieces of a 16 KiB tile buffer one wave moves: slot t lands
-// 4 KiB past slot t - 1 (pieces wave, wave + 4, wave + 8, wave + 12).
-__device__ __forceinline__ void load_four_slots(int4v rsrc, unsigned first, const int (&voffset)[4], int soffset) {
-    load_to_lds_at<0>(rsrc, first, voffset[0], soffset);
-    load_to_lds_at<4096>(rsrc, first, voffset[1], soffset);
-    load_to_lds_at<8192>(rsrc, first, voffset[2], soffset);
-    load_to_lds_at<12288>(rsrc, first, voffset[3], soffset);
+// The 1 KiB pieces one wave moves of a tile buffer that splits evenly over
+// the workgroup's four waves: slot t lands 4 KiB past slot t - 1 (pieces
+// wave, wave + 4, ...), so all slots share the first one's LDS address.
+template <int t, int kSlots>
+__device__ __forceinline__ void load_slots_from(int4v rsrc, unsigned first, const int (&voffset)[kSlots], int soffset) {
+    if constexpr (t < kSlots) {
+        load_to_lds_at<4096 * t>(rsrc, first, voffset[t], soffset);
+        load_slots_from<t + 1, kSlots>(rsrc, first, voffset, soffset);
+    }
+}
+template <int kSlots>
+__device__ __forceinline__ void load_slots(int4v rsrc, unsigned first, const int (&voffset)[kSlots], int soffset) {
+    load_slots_from<0, kSlots>(rsrc, first, voffset, soffset);
 }
 
 template <int DC, bool kVector, bool kPrecise, bool kDots>
@@ -471,16 +477,20 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         const int k0 = j * kTileKeys;
         if constexpr (kVector) {
             if (need16) {
-                if constexpr (L::kKLoads == 4 * kWavesPerGroup) {
-                    load_four_slots(rsrc_k, dst_k[0], off_k, k0 * k_row_bytes);
+                if constexpr (L::kKLoads % kWavesPerGroup == 0) {
+                    load_slots(rsrc_k, dst_k[0], off_k, k0 * k_row_bytes);
                 } else {
 #pragma unroll
                     for (int t = 0; t < L::kKPerWave; ++t) load_to_lds(rsrc_k, dst_k[t], off_k[t], k0 * k_row_bytes);
                 }
             }
             if (need8) {
+                if constexpr (L::kK8Loads % kWavesPerGroup == 0) {
+                    load_slots(rsrc_k8, dst_k8[0], off_k8, k0 * d);
+                } else {
 #pragma unroll
-                for (int t = 0; t < L::kK8PerWave; ++t) load_to_lds(rsrc_k8, dst_k8[t], off_k8[t], k0 * d);
+                    for (int t = 0; t < L::kK8PerWave; ++t) load_to_lds(rsrc_k8, dst_k8[t], off_k8[t], k0 * d);
+                }
             }
         } else {
             if (need16) {
@@ -502,8 +512,8 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     auto issue_v = [&](int j) {
         const int k0 = j * kTileKeys;
         if constexpr (kVector) {
-            if constexpr (L::kVLoads == 4 * kWavesPerGroup) {
-                load_four_slots(rsrc_v, dst_v[0], off_v, k0 * v_row_bytes);
+            if constexpr (L::kVLoads % kWavesPerGroup == 0) {
+                load_slots(rsrc_v, dst_v[0], off_v, k0 * v_row_bytes);
             } else {
 #pragma unroll
                 for (int t = 0; t < L::kVPerWave; ++t) load_to_lds(rsrc_v, dst_v[t], off_v[t], k0 * v_row_bytes);
