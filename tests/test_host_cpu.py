@@ -177,3 +177,19 @@ def test_pack_heads_concatenates_per_head_words():
     for h in range(4):
         decoded = oracle.decode_routes(route[h * per_head:(h + 1) * per_head], None, w.S, w.S, 2)
         assert np.array_equal(decoded, codes[h])
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py is a one-GPU benchmark: --gpus N > 1 exits with code 2 and a
+    JSON line naming the reason, before touching any device."""
+    import json
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    proc = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                          timeout=120, cwd=root)
+    assert proc.returncode == 2, proc.stderr
+    line = json.loads(proc.stdout.strip().splitlines()[-1])
+    assert "one GPU" in line["error"]
