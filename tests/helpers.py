@@ -53,6 +53,25 @@ def guarded(count: int, dtype, guard, fill=None):
     return dev(buffer)
 
 
+def guarded_lead(count: int, dtype, guard, fill=None, lead: int = 1):
+    """Device buffer of lead + count + 1 elements: `lead` guards, fill..., guard.
+    The payload starts lead * itemsize bytes in: lead = 1 for a 4-byte element
+    gives an output that is not 16-byte aligned (the kernels' element-wise
+    path), lead = 4 one that is (their 16-byte vector path)."""
+    buffer = np.full(count + lead + 1, guard if fill is None else fill, dtype=dtype)
+    buffer[:lead] = guard
+    buffer[-1] = guard
+    return dev(buffer)
+
+
+def nan_padded_rows(bits: np.ndarray, rows: int = 64) -> np.ndarray:
+    """A [n, d] fp16 bit array followed by `rows` rows of NaN (0x7E00): a
+    kernel that reads past row n - 1 (up to the end of its last 64-key tile)
+    turns the NaN into a NaN output, since 0 * NaN = NaN in P.V."""
+    bits = np.asarray(bits, dtype=np.uint16)
+    return np.concatenate([bits, np.full((rows,) + bits.shape[1:], 0x7E00, dtype=np.uint16)])
+
+
 def compare(actual: np.ndarray, expected: np.ndarray, atol: float, rtol: float, label: str) -> dict:
     """|a - e| <= atol + rtol |e| elementwise (src/tests/tilemix_test.cu:137-155)."""
     actual = np.asarray(actual, dtype=np.float64).reshape(-1)

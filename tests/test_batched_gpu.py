@@ -20,7 +20,7 @@ import math
 import numpy as np
 import pytest
 
-from helpers import GUARD_DOT, GUARD_F32, GUARD_TRACE, compare, dev, dev_half, guarded, host
+from helpers import GUARD_DOT, GUARD_F32, GUARD_TRACE, compare, dev, dev_half, guarded, guarded_lead, host
 
 pytestmark = pytest.mark.gpu
 
@@ -199,17 +199,24 @@ BATCH_CASES = [
 ]
 
 
-@pytest.mark.parametrize("heads,M,N,d,g,causal,p_skip", BATCH_CASES,
+# Each case runs with O at a 4-byte offset (element-wise path) and 16-byte
+# aligned (the vector path when d % 16 == 0); the 64 NaN rows between heads
+# cover every row a head's last 64-key tile could reach past N.
+BATCH_RUNS = [c + (aligned,) for c in BATCH_CASES for aligned in (False, True)]
+
+
+@pytest.mark.parametrize("heads,M,N,d,g,causal,p_skip,aligned", BATCH_RUNS,
                          ids=[f"h{c[0]}-{c[1]}x{c[2]}x{c[3]}-g{c[4]}{'-causal' if c[5] else ''}-skip{c[6]}"
-                              for c in BATCH_CASES])
-def test_batched_extensions_vs_oracle(tm, oracle_lib, cuda, heads, M, N, d, g, causal, p_skip):
+                              f"{'-aligned' if c[7] else ''}" for c in BATCH_RUNS])
+def test_batched_extensions_vs_oracle(tm, oracle_lib, cuda, heads, M, N, d, g, causal, p_skip, aligned):
     """Skip words, causal masking, ragged sizes, padded head strides, fused
     quantization (mode 1) with Q8/q_scales outputs, decoded route codes."""
     import torch
 
     from tilemix import routing
 
-    pad = 5
+    pad = 64
+    lead = 4 if aligned else 1
     q, k, v, Qp, Kp, Vp, rng = make_problem(oracle_lib, heads, M, N, d, seed=M * N + d, pad=pad)
     codes = np.stack([random_codes(rng, M, N, g, p_skip) for _ in range(heads)])
     if p_skip:
@@ -220,7 +227,7 @@ def test_batched_extensions_vs_oracle(tm, oracle_lib, cuda, heads, M, N, d, g, c
                             for s in skip_parts]) if p_skip else None)
     Q, K, V = dev_half(Qp), dev_half(Kp), dev_half(Vp)
     o_stride = (M + pad) * d
-    O = guarded(heads * o_stride, np.float32, GUARD_F32, fill=np.float32(777.0))
+    O = guarded_lead(heads * o_stride, np.float32, GUARD_F32, fill=np.float32(777.0), lead=lead)
     Q8 = torch.empty((heads, M, d), dtype=torch.int8, device="cuda:0")
     K8 = torch.empty((heads, N, d), dtype=torch.int8, device="cuda:0")
     qs = torch.empty((heads, (M + 127) // 128), dtype=torch.int16, device="cuda:0")
@@ -228,17 +235,19 @@ def test_batched_extensions_vs_oracle(tm, oracle_lib, cuda, heads, M, N, d, g, c
     cells = codes[0].size
     trace = guarded(heads * cells, np.uint8, GUARD_TRACE)
     scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
-    args = tm.BatchedArgs(Q=Q, K=K, V=V, O=O.data_ptr() + 4, heads=heads, M=M, N=N, d=d, score_scale=scale,
+    args = tm.BatchedArgs(Q=Q, K=K, V=V, O=O.data_ptr() + 4 * lead, heads=heads, M=M, N=N, d=d,
+                          score_scale=scale,
                           q_head_stride=(M + pad) * d, k_head_stride=(N + pad) * d, v_head_stride=(N + pad) * d,
                           o_head_stride=o_stride, causal=causal, quantize=1, route_words=dev(route),
                           skip_words=dev(skip) if skip is not None else None, key_tiles_per_group=g,
                           decoded_bits=trace.data_ptr() + 1, Q8=Q8, K8=K8, q_scales=qs, k_scales=ks)
-    print(f"batched heads={heads} M={M} N={N} d={d} g={g} causal={causal} p_skip={p_skip}", flush=True)
+    print(f"batched heads={heads} M={M} N={N} d={d} g={g} causal={causal} p_skip={p_skip} aligned={aligned}",
+          flush=True)
     tm.check(tm.attention_batched(args))
     torch.cuda.synchronize()
     out = host(O)
-    assert out[0] == GUARD_F32 and out[-1] == GUARD_F32, "output guard overwritten"
-    out = out[1:-1].reshape(heads, M + pad, d)
+    assert (out[:lead] == GUARD_F32).all() and out[-1] == GUARD_F32, "output guard overwritten"
+    out = out[lead:-1].reshape(heads, M + pad, d)
     assert (out[:, M:] == np.float32(777.0)).all(), "head padding of O written"
     got_trace = host(trace)
     assert got_trace[0] == GUARD_TRACE and got_trace[-1] == GUARD_TRACE

@@ -9,6 +9,7 @@ from __future__ import annotations
 import ctypes
 import os
 import re
+import shutil
 import subprocess
 import sys
 from pathlib import Path
@@ -195,14 +196,18 @@ def test_mask_producer_validation_codes(tm):
     assert tm.tiles_importance(fake, fake, 1, 16 * 20000, 64, 64, 16, 64, 0.25, fake, huge, fake) == NOT_SUPPORTED
 
 
+
 def test_missing_library_fails_loudly(tmp_path):
+    # A copy of the binding package with no library beside it: it must raise,
+    # not fall back to anything.
+    shutil.copytree(ROOT / "tilemix-cuda_amd" / "tilemix", tmp_path / "pkg" / "tilemix")
     code = ("import sys; sys.path.insert(0, %r)\n"
             "import tilemix\n"
+            "assert not tilemix.library_path().exists()\n"
             "try:\n    tilemix.library()\nexcept ImportError as e:\n    print('ImportError', e)\n"
-            % str(ROOT / "tilemix-cuda_amd"))
-    env = dict(os.environ, TILEMIX_HIP_LIBRARY=str(tmp_path / "absent.so"))
-    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
-    assert "ImportError" in out.stdout and "no fallback" in out.stdout
+            % str(tmp_path / "pkg"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert "ImportError" in out.stdout and "no fallback" in out.stdout, out.stderr
 
 
 def test_product_never_uses_the_oracle():

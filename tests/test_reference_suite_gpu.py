@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from helpers import (GUARD_DOT, GUARD_F32, GUARD_I8, GUARD_SCALE, GUARD_TRACE, compare, dev, dev_half,
-                     guarded, host, reference_group_words)
+                     guarded, guarded_lead, host, nan_padded_rows, reference_group_words)
 
 pytestmark = pytest.mark.gpu
 
@@ -46,26 +46,42 @@ def _stream(default_stream: bool, torch_stream):
     return None if default_stream else torch_stream
 
 
-@pytest.mark.parametrize("m,n,d,pattern,default_stream", DENSE_CASES,
-                         ids=[f"{c[0]}x{c[1]}x{c[2]}-{c[3]}{'-default' if c[4] else ''}" for c in DENSE_CASES])
-def test_dense_case(tm, oracle_lib, cuda, torch_stream, m, n, d, pattern, default_stream):
+# Every case runs with O at a 4-byte offset (the element-wise path) and, where
+# d % 16 == 0, again with O 16-byte aligned (the 16-byte vector path with LDS
+# DMA tile loads). K and V are followed by 64 NaN rows inside their
+# allocation, so a read past row N - 1 shows up as NaN in O.
+DENSE_RUNS = [(c, aligned) for c in DENSE_CASES for aligned in (False, True) if not aligned or c[2] % 16 == 0]
+
+
+def _dense_id(run):
+    (m, n, d, pattern, default), aligned = run
+    return f"{m}x{n}x{d}-{pattern}{'-default' if default else ''}{'-aligned' if aligned else ''}"
+
+
+@pytest.mark.parametrize("run", DENSE_RUNS, ids=[_dense_id(r) for r in DENSE_RUNS])
+def test_dense_case(tm, oracle_lib, cuda, torch_stream, run):
     import torch
 
+    (m, n, d, pattern, default_stream), aligned = run
+    lead = 4 if aligned else 1
     q, k, v = oracle_lib.make_inputs(m, n, d, pattern)
     expected = oracle_lib.attention(q, k, v)
-    dq, dk, dv = dev_half(q), dev_half(k), dev_half(v)
-    out = guarded(m * d, np.float32, GUARD_F32, fill=np.nan)
+    dq = dev_half(q)
+    dk, dv = dev_half(nan_padded_rows(k.reshape(n, d))), dev_half(nan_padded_rows(v.reshape(n, d)))
+    out = guarded_lead(m * d, np.float32, GUARD_F32, fill=np.nan, lead=lead)
     stream = _stream(default_stream, torch_stream)
-    print(f"dense case M={m} N={n} d={d} pattern={pattern}", flush=True)
+    print(f"dense case M={m} N={n} d={d} pattern={pattern} aligned={aligned}", flush=True)
     scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))  # 1.0f / std::sqrt(float(d))
-    code = tm.launch_fused_fp16_attention(dq, dk, dv, out.data_ptr() + 4, m, n, d, scale, stream)
+    code = tm.launch_fused_fp16_attention(dq, dk, dv, out.data_ptr() + 4 * lead, m, n, d, scale, stream)
     assert code == tm.SUCCESS
     torch.cuda.synchronize()
     result = host(out)
-    assert result[0] == GUARD_F32 and result[-1] == GUARD_F32, "output guard overwritten"
-    compare(result[1:-1], expected, 1e-5, 1e-4, f"TileMix vs fp64 M={m} N={n} d={d} {pattern}")
-    for device_tensor, original in ((dq, q), (dk, k), (dv, v)):
-        assert np.array_equal(host(device_tensor), original), "kernel modified a Q/K/V input"
+    assert (result[:lead] == GUARD_F32).all() and result[-1] == GUARD_F32, "output guard overwritten"
+    compare(result[lead:-1], expected, 1e-5, 1e-4, f"TileMix vs fp64 M={m} N={n} d={d} {pattern}")
+    assert np.array_equal(host(dq), q), "kernel modified the Q input"
+    for device_tensor, original in ((dk, k), (dv, v)):
+        assert np.array_equal(host(device_tensor).reshape(-1)[: n * d], original.reshape(-1)), \
+            "kernel modified a K/V input"
 
 
 def test_score_scale_reuse(tm, cuda, torch_stream):
@@ -154,10 +170,17 @@ def _routing_id(case):
     return f"{m}x{n}x{d}-{inputs}-g{g}-{pattern}{'' if trace else '-notrace'}{'-default' if default else ''}"
 
 
-@pytest.mark.parametrize("case", ROUTING_CASES, ids=[_routing_id(c) for c in ROUTING_CASES])
-def test_routing_case(tm, oracle_lib, cuda, torch_stream, case):
+ROUTING_RUNS = [(c, aligned) for c in ROUTING_CASES for aligned in (False, True)
+                if not aligned or c[0][2] % 16 == 0]
+
+
+@pytest.mark.parametrize("run", ROUTING_RUNS,
+                         ids=[_routing_id(c) + ("-aligned" if a else "") for c, a in ROUTING_RUNS])
+def test_routing_case(tm, oracle_lib, cuda, torch_stream, run):
     import torch
 
+    case, aligned = run
+    lead = 4 if aligned else 1
     (m, n, d, inputs, default_stream), group, pattern, trace = case
     query_tiles, key_tiles = (m + 15) // 16, (n + 31) // 32
     implicit = pattern == "implicit-fp16"
@@ -167,8 +190,10 @@ def test_routing_case(tm, oracle_lib, cuda, torch_stream, case):
     q8_ref, qs_ref = oracle_lib.quantize(q, 128)
     k8_ref, ks_ref = oracle_lib.quantize(k, 64)
     stream = _stream(default_stream, torch_stream)
-    dq, dk, dv = dev_half(q), dev_half(k), dev_half(v)
-    out = guarded(m * d, np.float32, GUARD_F32, fill=np.nan)
+    dq = dev_half(q)
+    # K / V with 64 NaN rows after row N - 1 (see DENSE_RUNS); quantized from the first N rows.
+    dk, dv = dev_half(nan_padded_rows(k.reshape(n, d))), dev_half(nan_padded_rows(v.reshape(n, d)))
+    out = guarded_lead(m * d, np.float32, GUARD_F32, fill=np.nan, lead=lead)
     mask = dev(words)
     bits = guarded(expected_bits.size, np.uint8, GUARD_TRACE)
     q8 = torch.empty(q.size, dtype=torch.int8, device="cuda:0")
@@ -176,21 +201,23 @@ def test_routing_case(tm, oracle_lib, cuda, torch_stream, case):
     q_scales = torch.empty(qs_ref.size, dtype=torch.int16, device="cuda:0")
     k_scales = torch.empty(ks_ref.size, dtype=torch.int16, device="cuda:0")
     dots = guarded(m * n, np.int32, GUARD_DOT)
-    print(f"routing case M={m} N={n} d={d} g={group} pattern={pattern} trace={trace}", flush=True)
+    print(f"routing case M={m} N={n} d={d} g={group} pattern={pattern} trace={trace} aligned={aligned}",
+          flush=True)
     assert tm.quantize_tilemix_qk(dq, dk, q8, k8, q_scales, k_scales, m, n, d, stream) == tm.SUCCESS
     scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
     # All-FP16 masks must preserve the un-routed result exactly (:490-509).
-    assert tm.launch_fused_fp16_attention(dq, dk, dv, out.data_ptr() + 4, m, n, d, scale, stream) == tm.SUCCESS
+    assert tm.launch_fused_fp16_attention(dq, dk, dv, out.data_ptr() + 4 * lead, m, n, d, scale,
+                                          stream) == tm.SUCCESS
     torch.cuda.synchronize()
     baseline = host(out)
     routing = tm.TileMixRouting(None if implicit else mask, 0 if implicit else words.size, group,
                                 bits.data_ptr() + 1 if trace else None)
     quantized = tm.TileMixQuantized(q8, k8, q_scales, k_scales, dots.data_ptr() + 4)
-    assert tm.launch_fused_fp16_attention(dq, dk, dv, out.data_ptr() + 4, m, n, d, scale, stream,
+    assert tm.launch_fused_fp16_attention(dq, dk, dv, out.data_ptr() + 4 * lead, m, n, d, scale, stream,
                                           routing, quantized) == tm.SUCCESS
     torch.cuda.synchronize()
     actual = host(out)
-    assert actual[0] == GUARD_F32 and actual[-1] == GUARD_F32, "routed output guard overwritten"
+    assert (actual[:lead] == GUARD_F32).all() and actual[-1] == GUARD_F32, "routed output guard overwritten"
     if not expected_bits.any():
         assert np.array_equal(actual.view(np.uint32), baseline.view(np.uint32)), \
             "all-FP16 routing changed baseline outputs"
@@ -210,4 +237,4 @@ def test_routing_case(tm, oracle_lib, cuda, torch_stream, case):
     assert np.array_equal(host(q_scales).view(np.uint16), qs_ref)
     assert np.array_equal(host(k_scales).view(np.uint16), ks_ref)
     mixed = oracle_lib.tilemix(q, k, v, q8_ref, k8_ref, qs_ref, ks_ref, expected_bits, scale)
-    compare(actual[1:-1], mixed, 1e-5, 1e-4, "mixed FP16/INT8 vs fp64 TileMix oracle")
+    compare(actual[lead:-1], mixed, 1e-5, 1e-4, "mixed FP16/INT8 vs fp64 TileMix oracle")

@@ -214,7 +214,7 @@ __device__ __forceinline__ void load_to_lds_at(int4v rsrc, unsigned lds_address,
         asm volatile("s_add_u32 m0, %0, %4\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                      :
                      : "s"(lds_address), "v"(voffset), "s"(rsrc), "s"(soffset), "i"(kOffset)
-                     : "memory");
+                     : "memory", "scc");
     }
 }
 
@@ -472,25 +472,46 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             dst_k8[t] = w < L::kK8Loads ? lds_k8_address + 1024 * w : lds_spare_address;
         }
     }
+    // Tile DMA of one buffer: every slot of this wave from resource r at
+    // scalar offset soffset. A tile that runs past the last key (the head's
+    // last tile when N % 64 != 0) is issued through a view starting at the
+    // tile (rsrc_from), so that its rows past N fail the range check.
+    auto k_slots = [&](int4v r, int soffset) {
+        if constexpr (L::kKLoads % kWavesPerGroup == 0) {
+            load_slots(r, dst_k[0], off_k, soffset);
+        } else {
+#pragma unroll
+            for (int t = 0; t < L::kKPerWave; ++t) load_to_lds(r, dst_k[t], off_k[t], soffset);
+        }
+    };
+    auto k8_slots = [&](int4v r, int soffset) {
+        if constexpr (L::kK8Loads % kWavesPerGroup == 0) {
+            load_slots(r, dst_k8[0], off_k8, soffset);
+        } else {
+#pragma unroll
+            for (int t = 0; t < L::kK8PerWave; ++t) load_to_lds(r, dst_k8[t], off_k8[t], soffset);
+        }
+    };
+    auto v_slots = [&](int4v r, int soffset) {
+        if constexpr (L::kVLoads % kWavesPerGroup == 0) {
+            load_slots(r, dst_v[0], off_v, soffset);
+        } else {
+#pragma unroll
+            for (int t = 0; t < L::kVPerWave; ++t) load_to_lds(r, dst_v[t], off_v[t], soffset);
+        }
+    };
     // K (FP16 cells) and K8 (INT8 cells) of tile j.
     auto issue_k = [&](int j, bool need16, bool need8) {
         const int k0 = j * kTileKeys;
         if constexpr (kVector) {
+            const bool tail = k0 + kTileKeys > N;
             if (need16) {
-                if constexpr (L::kKLoads % kWavesPerGroup == 0) {
-                    load_slots(rsrc_k, dst_k[0], off_k, k0 * k_row_bytes);
-                } else {
-#pragma unroll
-                    for (int t = 0; t < L::kKPerWave; ++t) load_to_lds(rsrc_k, dst_k[t], off_k[t], k0 * k_row_bytes);
-                }
+                if (tail) k_slots(rsrc_from(rsrc_k, k0 * k_row_bytes), 0);
+                else k_slots(rsrc_k, k0 * k_row_bytes);
             }
             if (need8) {
-                if constexpr (L::kK8Loads % kWavesPerGroup == 0) {
-                    load_slots(rsrc_k8, dst_k8[0], off_k8, k0 * d);
-                } else {
-#pragma unroll
-                    for (int t = 0; t < L::kK8PerWave; ++t) load_to_lds(rsrc_k8, dst_k8[t], off_k8[t], k0 * d);
-                }
+                if (tail) k8_slots(rsrc_from(rsrc_k8, k0 * d), 0);
+                else k8_slots(rsrc_k8, k0 * d);
             }
         } else {
             if (need16) {
@@ -512,12 +533,8 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     auto issue_v = [&](int j) {
         const int k0 = j * kTileKeys;
         if constexpr (kVector) {
-            if constexpr (L::kVLoads % kWavesPerGroup == 0) {
-                load_slots(rsrc_v, dst_v[0], off_v, k0 * v_row_bytes);
-            } else {
-#pragma unroll
-                for (int t = 0; t < L::kVPerWave; ++t) load_to_lds(rsrc_v, dst_v[t], off_v[t], k0 * v_row_bytes);
-            }
+            if (k0 + kTileKeys > N) v_slots(rsrc_from(rsrc_v, k0 * v_row_bytes), 0);
+            else v_slots(rsrc_v, k0 * v_row_bytes);
         } else {
             for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
                 const int row = e / kDP, f = e % kDP, key = k0 + row;
@@ -1033,6 +1050,10 @@ extern "C" int tilemix_attention_batched(const TileMixBatchedArgs* args, void* s
     } else if (a.score_dots) {
         return hipErrorInvalidValue;
     }
+    // Every check precedes the first launch: an error return leaves all
+    // outputs (K8 / k_scales of the pre-pass included) untouched.
+    if (static_cast<long long>((a.M - 1) / kQBlockRows + 1) * a.heads > 0x7fffffffLL)
+        return hipErrorInvalidConfiguration;
     if (a.quantize == 1 && int8) {
         const QuantSide none = make_quant_side(nullptr, nullptr, nullptr, 0, 1, kQBlockRows, a.d);
         const QuantSide k = make_quant_side(a.K, a.K8, a.k_scales, a.k_head_stride, a.N, kKBlockRows, k_row);

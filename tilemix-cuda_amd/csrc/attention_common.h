@@ -133,6 +133,20 @@ __device__ __forceinline__ int4v make_rsrc(const void* base, int bytes) {
                  __builtin_amdgcn_readfirstlane(bytes), static_cast<int>(kBufferFlags)};
 }
 
+// The same buffer viewed from byte `offset` on (0 <= offset < the range):
+// base + offset, range - offset. The range check covers the per-lane offset
+// only (the scalar offset of a buffer load is not range-checked on gfx9
+// family parts), so a tile whose rows run past the end of a head is
+// addressed through a view that starts at the tile: its rows past the end
+// then fail the check and read as zero instead of reading past the head.
+__device__ __forceinline__ int4v rsrc_from(int4v rsrc, int offset) {
+    const unsigned long long base = static_cast<unsigned>(rsrc[0]) |
+                                    (static_cast<unsigned long long>(static_cast<unsigned>(rsrc[1]) & 0xffffu) << 32);
+    const unsigned long long moved = base + static_cast<unsigned>(offset);
+    return int4v{static_cast<int>(moved & 0xffffffffu), static_cast<int>((moved >> 32) & 0xffffu),
+                 rsrc[2] - offset, rsrc[3]};
+}
+
 // LDS byte address of a workgroup-shared buffer, for M0 of an LDS DMA. The
 // cast from a generic pointer carries a null check (two scalar instructions),
 // so kernels convert each buffer's base once and add offsets to the result.

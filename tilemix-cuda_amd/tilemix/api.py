@@ -2,7 +2,6 @@
 from __future__ import annotations
 
 import ctypes
-import os
 from dataclasses import dataclass
 from pathlib import Path
 from typing import Any, Optional
@@ -24,9 +23,8 @@ class TileMixError(RuntimeError):
 
 
 def library_path() -> Path:
-    """The in-tree build, or the file named by TILEMIX_HIP_LIBRARY (an alternative build)."""
-    override = os.environ.get("TILEMIX_HIP_LIBRARY")
-    return Path(override) if override else _PACKAGE_DIR / _LIB_NAME
+    """The in-tree build (tilemix-cuda_amd/libtilemix_hip.so)."""
+    return _PACKAGE_DIR / _LIB_NAME
 
 
 # Element types of O (include/tilemix_capi.h TILEMIX_DTYPE_*).
@@ -115,8 +113,19 @@ def _ptr(x: Any) -> Optional[int]:
 
 
 def _stream(stream: Any) -> Optional[int]:
+    """hipStream_t of `stream`: a torch stream, an int handle (0 = the null
+    stream), or None = torch's current stream on the current device (as torch
+    ops would use), so that a call inside `with torch.cuda.stream(s):` is
+    ordered after the kernels that produced its inputs. Before torch has
+    initialised the GPU no torch stream can be current: None is then the null
+    stream."""
     if stream is None:
-        return None
+        import sys
+
+        torch = sys.modules.get("torch")
+        if torch is None or not torch.cuda.is_initialized():
+            return None
+        return torch.cuda.current_stream().cuda_stream or None
     if isinstance(stream, int):
         return stream or None
     return stream.cuda_stream or None
@@ -290,4 +299,3 @@ def tiles_importance(Q, K, heads: int, M: int, N: int, d: int, tile_rows: int, t
                                               k_head_stride or N * d, tile_rows, tile_keys, fp16_fraction,
                                               _ptr(workspace), workspace_bytes, _ptr(tile_codes),
                                               _stream(stream))
-
