@@ -8,7 +8,9 @@
  *   - fp16 tensors are passed as `uint16_t*` holding IEEE binary16 bit
  *     patterns (the storage of `__half`);
  *   - every pointer is a device pointer owned by the caller; the library
- *     allocates nothing and keeps no state between calls;
+ *     allocates nothing and keeps no state between calls (a cached
+ *     per-device capability check and the fixed scratch array of
+ *     tilemix_tiles_importance_noalloc aside);
  *   - `stream` is a `hipStream_t` (NULL = the default stream); all work is
  *     enqueued on it and nothing synchronises;
  *   - the return value is a `hipError_t` code (0 = hipSuccess). Argument
@@ -213,6 +215,22 @@ int tilemix_tiles_importance(const uint16_t* Q, const uint16_t* K, int heads, in
                              int64_t q_head_stride, int64_t k_head_stride, int tile_rows, int tile_keys,
                              float fp16_fraction, float* workspace, size_t workspace_bytes,
                              uint8_t* tile_codes, void* stream);
+
+/* tilemix_tiles_importance without a workspace argument: no reference
+ * counterpart. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * the per-tile maxima live in a fixed scratch array inside the library, one
+ * copy per GPU (tilemix_importance_noalloc_max_bytes(), 1 MiB), located once
+ * per device with hipGetSymbolAddress on the first call there; the call
+ * allocates nothing. Problems needing more than that
+ * (tilemix_importance_workspace_bytes(...) > the maximum) -> InvalidValue;
+ * other errors as tilemix_tiles_importance. Every call on one GPU shares the
+ * scratch, so calls that overlap on one GPU (different streams, threads)
+ * race; calls ordered on one stream do not. */
+size_t tilemix_importance_noalloc_max_bytes(void);
+int tilemix_tiles_importance_noalloc(const uint16_t* Q, const uint16_t* K, int heads, int M, int N, int d,
+                                     int64_t q_head_stride, int64_t k_head_stride, int tile_rows, int tile_keys,
+                                     float fp16_fraction, uint8_t* tile_codes, void* stream);
 
 /* tilemix_quantize_qk_batched with row strides (elements between consecutive
  * rows of a head, 0 = d) for row-strided Q/K such as [B, S, H, D] tensors;

@@ -194,7 +194,16 @@ def test_mask_producer_validation_codes(tm):
                                q_head_stride=100) == INVALID                        # overlapping heads
     huge = tm.importance_workspace_bytes(1, 16 * 20000, 64, 16, 64)
     assert tm.tiles_importance(fake, fake, 1, 16 * 20000, 64, 64, 16, 64, 0.25, fake, huge, fake) == NOT_SUPPORTED
-
+    # allocation-free importance router: its fixed scratch bounds the problem
+    assert tm.importance_noalloc_max_bytes() == 1 << 20
+    assert tm.importance_workspace_bytes(1024, 16384, 16384, 128, 64) > tm.importance_noalloc_max_bytes()
+    assert tm.tiles_importance_noalloc(fake, fake, 1024, 16384, 16384, 128, 128, 64, 0.25, fake) == INVALID
+    assert tm.tiles_importance_noalloc(None, fake, 2, 256, 256, 64, 128, 64, 0.25, fake) == INVALID
+    assert tm.tiles_importance_noalloc(fake, fake, 2, 256, 256, 64, 128, 64, 1.25, fake) == INVALID
+    assert tm.tiles_importance_noalloc(fake, fake, 2, 256, 256, 64, 128, 64, 0.25, None) == INVALID
+    assert tm.tiles_importance_noalloc(fake, fake, 2, 256, 256, 64, 128, 64, 0.25, fake,
+                                       q_head_stride=100) == INVALID                # overlapping heads
+    assert tm.tiles_importance_noalloc(fake, fake, 1, 16 * 20000, 64, 64, 16, 64, 0.25, fake) == NOT_SUPPORTED
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -25,6 +25,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 
 namespace tilemix {
 namespace {
@@ -322,25 +323,66 @@ extern "C" std::size_t tilemix_importance_workspace_bytes(int heads, int M, int 
     return static_cast<std::size_t>(heads) * entries * sizeof(float);
 }
 
-extern "C" int tilemix_tiles_importance(const std::uint16_t* Q, const std::uint16_t* K, int heads, int M, int N,
-                                        int d, std::int64_t q_head_stride, std::int64_t k_head_stride,
-                                        int tile_rows, int tile_keys, float fp16_fraction, float* workspace,
-                                        std::size_t workspace_bytes, std::uint8_t* tile_codes, void* stream) {
-    using namespace tilemix;
-    if (!Q || !K || !workspace || !tile_codes || heads <= 0 || M <= 0 || N <= 0 || d <= 0 ||
+// Scratch of tilemix_tiles_importance_noalloc: the per-tile maxima of up to
+// kImportanceScratchFloats / (tiles_q + tiles_k) heads. One copy per GPU,
+// held until the process ends; every call on a GPU shares it, so calls that
+// overlap on one GPU race.
+static constexpr std::size_t kImportanceScratchFloats = std::size_t{1} << 18;  // 1 MiB
+static __device__ __align__(256) float scratch[kImportanceScratchFloats];
+
+namespace tilemix {
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current (in host code the array's name is only a
+// host-side stand-in, not a device address).
+hipError_t scratch_address(float** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex lock;
+    static float* address[kMaxDevices] = {};
+    int device = 0;
+    hipError_t status = hipGetDevice(&device);
+    if (status != hipSuccess) return status;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> guard(lock);
+    if (!address[device]) {
+        void* ptr = nullptr;
+        status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (status != hipSuccess) return status;
+        address[device] = static_cast<float*>(ptr);
+    }
+    *out = address[device];
+    return hipSuccess;
+}
+
+// Argument checks shared by both importance entry points, in two groups so
+// that each entry point can keep its order (no runtime call): values first
+// (InvalidValue), limits after the caller's own buffer-size check.
+bool importance_values_ok(const std::uint16_t* Q, const std::uint16_t* K, int heads, int M, int N, int d,
+                          std::int64_t q_head_stride, std::int64_t k_head_stride, int tile_rows, int tile_keys,
+                          float fp16_fraction, const std::uint8_t* tile_codes) {
+    if (!Q || !K || !tile_codes || heads <= 0 || M <= 0 || N <= 0 || d <= 0 ||
         !tile_shape_ok(tile_rows, tile_keys) || !probability_ok(fp16_fraction))
-        return hipErrorInvalidValue;
-    if (heads > 1 && (q_head_stride < static_cast<std::int64_t>(M) * d || k_head_stride < static_cast<std::int64_t>(N) * d))
-        return hipErrorInvalidValue;
-    if (workspace_bytes < tilemix_importance_workspace_bytes(heads, M, N, tile_rows, tile_keys))
-        return hipErrorInvalidValue;
+        return false;
+    return heads == 1 || (q_head_stride >= static_cast<std::int64_t>(M) * d &&
+                          k_head_stride >= static_cast<std::int64_t>(N) * d);
+}
+
+hipError_t importance_limits(int heads, int M, int N, int tile_rows, int tile_keys) {
     const int tiles_q = (M - 1) / tile_rows + 1, tiles_k = (N - 1) / tile_keys + 1;
     if (tiles_q + tiles_k > kMaxSelectEntries) return hipErrorNotSupported;
     if (heads > 65535) return hipErrorInvalidConfiguration;
+    return hipSuccess;
+}
+
+// Tile maxima into `workspace`, then the per-head select into tile_codes.
+hipError_t launch_importance(const std::uint16_t* Q, const std::uint16_t* K, int heads, int M, int N, int d,
+                             std::int64_t q_head_stride, std::int64_t k_head_stride, int tile_rows, int tile_keys,
+                             float fp16_fraction, float* workspace, std::uint8_t* tile_codes, hipStream_t s) {
+    const int tiles_q = (M - 1) / tile_rows + 1, tiles_k = (N - 1) / tile_keys + 1;
     const std::int64_t total = static_cast<std::int64_t>(tiles_q) * tiles_k;
     // The number of FP16 tiles: fp16_fraction * total rounded half to even.
     const std::int64_t count = static_cast<std::int64_t>(std::nearbyint(static_cast<double>(fp16_fraction) * total));
-    const hipStream_t s = static_cast<hipStream_t>(stream);
     const std::int64_t qs = heads > 1 ? q_head_stride : static_cast<std::int64_t>(M) * d;
     const std::int64_t ks = heads > 1 ? k_head_stride : static_cast<std::int64_t>(N) * d;
     tile_absmax_kernel<<<dim3(static_cast<unsigned>(tiles_q + tiles_k), static_cast<unsigned>(heads)), 256, 0, s>>>(
@@ -351,4 +393,49 @@ extern "C" int tilemix_tiles_importance(const std::uint16_t* Q, const std::uint1
                                static_cast<std::size_t>(tiles_q + tiles_k) * sizeof(float), s>>>(
         workspace, tiles_q, tiles_k, count, tile_codes);
     return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace tilemix
+
+extern "C" int tilemix_tiles_importance(const std::uint16_t* Q, const std::uint16_t* K, int heads, int M, int N,
+                                        int d, std::int64_t q_head_stride, std::int64_t k_head_stride,
+                                        int tile_rows, int tile_keys, float fp16_fraction, float* workspace,
+                                        std::size_t workspace_bytes, std::uint8_t* tile_codes, void* stream) {
+    using namespace tilemix;
+    if (!workspace || !importance_values_ok(Q, K, heads, M, N, d, q_head_stride, k_head_stride, tile_rows,
+                                            tile_keys, fp16_fraction, tile_codes))
+        return hipErrorInvalidValue;
+    if (workspace_bytes < tilemix_importance_workspace_bytes(heads, M, N, tile_rows, tile_keys))
+        return hipErrorInvalidValue;
+    const hipError_t limits = importance_limits(heads, M, N, tile_rows, tile_keys);
+    if (limits != hipSuccess) return limits;
+    return launch_importance(Q, K, heads, M, N, d, q_head_stride, k_head_stride, tile_rows, tile_keys,
+                             fp16_fraction, workspace, tile_codes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" std::size_t tilemix_importance_noalloc_max_bytes(void) {
+    return kImportanceScratchFloats * sizeof(float);
+}
+
+extern "C" int tilemix_tiles_importance_noalloc(const std::uint16_t* Q, const std::uint16_t* K, int heads, int M,
+                                                int N, int d, std::int64_t q_head_stride,
+                                                std::int64_t k_head_stride, int tile_rows, int tile_keys,
+                                                float fp16_fraction, std::uint8_t* tile_codes, void* stream) {
+    using namespace tilemix;
+    if (!importance_values_ok(Q, K, heads, M, N, d, q_head_stride, k_head_stride, tile_rows, tile_keys,
+                              fp16_fraction, tile_codes))
+        return hipErrorInvalidValue;
+    // More tile maxima than the fixed scratch holds.
+    if (tilemix_importance_workspace_bytes(heads, M, N, tile_rows, tile_keys) > tilemix_importance_noalloc_max_bytes())
+        return hipErrorInvalidValue;
+    const hipError_t limits = importance_limits(heads, M, N, tile_rows, tile_keys);
+    if (limits != hipSuccess) return limits;
+    float* workspace = nullptr;
+    const hipError_t found = scratch_address(&workspace);
+    if (found != hipSuccess) return found;
+    // The tile-maxima kernel writes every entry the select reads, so the
+    // previous call's contents need no clearing.
+    return launch_importance(Q, K, heads, M, N, d, q_head_stride, k_head_stride, tile_rows, tile_keys,
+                             fp16_fraction, workspace, tile_codes, static_cast<hipStream_t>(stream));
 }

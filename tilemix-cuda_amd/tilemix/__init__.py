@@ -27,11 +27,13 @@ from .api import (  # noqa: F401
     DTYPE_F32,
     DTYPE_F16,
     DTYPE_BF16,
+    importance_noalloc_max_bytes,
     importance_workspace_bytes,
     routes_from_tiles,
     tiles_bernoulli,
     tiles_causal_band,
     tiles_importance,
+    tiles_importance_noalloc,
     tiles_three_way,
     routing_word_count,
     routing_words_per_row,

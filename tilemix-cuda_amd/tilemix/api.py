@@ -99,6 +99,10 @@ def library() -> ctypes.CDLL:
         so.tilemix_tiles_importance.argtypes = [vp, vp, i32, i32, i32, i32, i64, i64, i32, i32, f32, vp, sz,
                                                 vp, vp]
         so.tilemix_tiles_importance.restype = i32
+        so.tilemix_importance_noalloc_max_bytes.argtypes = []
+        so.tilemix_importance_noalloc_max_bytes.restype = sz
+        so.tilemix_tiles_importance_noalloc.argtypes = [vp, vp, i32, i32, i32, i32, i64, i64, i32, i32, f32, vp, vp]
+        so.tilemix_tiles_importance_noalloc.restype = i32
         _lib = so
     return _lib
 
@@ -299,3 +303,18 @@ def tiles_importance(Q, K, heads: int, M: int, N: int, d: int, tile_rows: int, t
                                               k_head_stride or N * d, tile_rows, tile_keys, fp16_fraction,
                                               _ptr(workspace), workspace_bytes, _ptr(tile_codes),
                                               _stream(stream))
+
+
+def importance_noalloc_max_bytes() -> int:
+    """Size of the library's fixed scratch used by tiles_importance_noalloc."""
+    return int(library().tilemix_importance_noalloc_max_bytes())
+
+
+def tiles_importance_noalloc(Q, K, heads: int, M: int, N: int, d: int, tile_rows: int, tile_keys: int,
+                             fp16_fraction: float, tile_codes, q_head_stride: int = 0, k_head_stride: int = 0,
+                             stream=None) -> int:
+    """tiles_importance without a workspace (the library's fixed scratch; the
+    call allocates no device memory). Calls that overlap on one GPU race."""
+    return library().tilemix_tiles_importance_noalloc(_ptr(Q), _ptr(K), heads, M, N, d, q_head_stride or M * d,
+                                                      k_head_stride or N * d, tile_rows, tile_keys,
+                                                      fp16_fraction, _ptr(tile_codes), _stream(stream))
