@@ -153,9 +153,10 @@ struct RowState {
 
 // x[b][kb] holds the 16 scores of query row i of block b for keys
 // 16kb + 4g + r; c is the per-tile log2-domain factor (>= 0); explicit scores
-// pass c = 1. Both blocks of the wave are handled together: one pass of row
-// maxima (the cross-lane steps of the two blocks interleave) and one
-// wave-uniform branch for the rare rescale.
+// pass c = 1. Both blocks of the wave are handled together: each lane's
+// maximum of its 16 scores, one wave-uniform branch for the rare rescale, and
+// there one pass of row maxima (the cross-lane steps of the two blocks
+// interleave).
 template <int kFB, bool kPrecise>
 __device__ __forceinline__ void softmax_tile(RowState<kFB>& st, const float4v (&x)[2][4], float c,
                                              half8 (&ph)[2][2], half8 (&pl)[2][2]) {
@@ -168,9 +169,12 @@ __device__ __forceinline__ void softmax_tile(RowState<kFB>& st, const float4v (&
         const float t3 = max3(x[b][3][0], x[b][3][1], x[b][3][2]);
         tile[b] = max3(max3(t0, t1, t2), t3, t3) * c;  // c >= 0: max(x) * c == max(x * c)
     }
-    row_max4_pair(tile[0], tile[1]);
+    // A row's maximum exceeds m + kLazyRescale exactly when one of its four
+    // lanes' own maxima does, so the row maxima (two cross-lane steps) are
+    // formed only on the rare tiles that raise the running maximum.
     const bool raise0 = tile[0] > st.m[0] + kLazyRescale, raise1 = tile[1] > st.m[1] + kLazyRescale;
     if (__any(raise0 || raise1)) {
+        row_max4_pair(tile[0], tile[1]);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             // Rows with no visible key yet keep m = -inf (their sums are still 0).
@@ -405,35 +409,44 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     }
 
     // ------------------------------------------------------ routing masks
-    // Lane c < 16 decodes cell (row c / 2, key half c % 2) of each tile from
-    // the route / skip word it keeps for its query tile; the word is reloaded
-    // only when the tile's group crosses into the next 64-group block. The
-    // ballots make the masks wave-uniform: bit 2r + t <-> cell (r, t).
+    // One pass decodes four tiles: lane 16t + c decodes cell c (row c / 2,
+    // key half c % 2) of tile jb + t from the route / skip word it keeps for
+    // its query tile; the word is reloaded only when the tile's group crosses
+    // into the next 64-group block. The two 64-bit ballots hold the four
+    // tiles' wave-uniform masks, bit 16t + 2r + h <-> tile jb + t, cell (r, h).
     const int qt0 = q0 / 16;
     const int my_qt = qt0 + ((lane & 15) >> 1);
-    const bool my_row_valid = lane < 16 && my_qt < p.q_tiles16;
+    const bool my_row_valid = my_qt < p.q_tiles16;
     const std::int64_t my_word_base =
         head * p.words_per_head + static_cast<std::int64_t>(my_qt) * p.words_per_row;
     std::int64_t cached_block = -1;
     std::uint64_t cached_route = 0, cached_skip = 0;
+    std::uint64_t batch_int8 = 0, batch_skip = 0;
+    int batch_first = -4;
     auto tile_masks = [&](int j, std::uint32_t& int8_mask, std::uint32_t& skip_mask) {
-        const int kt = 2 * j + (lane & 1);
-        bool skip = true, int8 = false;
-        if (my_row_valid && kt < p.key_tiles32) {
-            const unsigned group = p.group_shift >= 0 ? static_cast<unsigned>(kt) >> p.group_shift
-                                                      : static_cast<unsigned>(kt) / static_cast<unsigned>(p.key_tiles_per_group);
-            const std::int64_t block = group >> 6;
-            if (block != cached_block) {
-                cached_block = block;
-                cached_route = p.route_words ? p.route_words[my_word_base + block] : 0ull;
-                cached_skip = p.skip_words ? p.skip_words[my_word_base + block] : 0ull;
+        if (j >= batch_first + 4) {
+            batch_first = j;
+            const int kt = 2 * (j + (lane >> 4)) + (lane & 1);
+            bool skip = true, int8 = false;
+            if (my_row_valid && kt < p.key_tiles32) {
+                const unsigned group = p.group_shift >= 0 ? static_cast<unsigned>(kt) >> p.group_shift
+                                                          : static_cast<unsigned>(kt) / static_cast<unsigned>(p.key_tiles_per_group);
+                const std::int64_t block = group >> 6;
+                if (block != cached_block) {
+                    cached_block = block;
+                    cached_route = p.route_words ? p.route_words[my_word_base + block] : 0ull;
+                    cached_skip = p.skip_words ? p.skip_words[my_word_base + block] : 0ull;
+                }
+                const unsigned bit = static_cast<unsigned>(group & 63);
+                skip = (cached_skip >> bit) & 1u;
+                int8 = !skip && ((cached_route >> bit) & 1u);
             }
-            const unsigned bit = static_cast<unsigned>(group & 63);
-            skip = (cached_skip >> bit) & 1u;
-            int8 = !skip && ((cached_route >> bit) & 1u);
+            batch_int8 = __ballot(int8);
+            batch_skip = __ballot(skip);
         }
-        int8_mask = static_cast<std::uint32_t>(__ballot(lane < 16 && int8));
-        skip_mask = static_cast<std::uint32_t>(__ballot(lane < 16 && skip));
+        const int shift = 16 * (j - batch_first);
+        int8_mask = static_cast<std::uint32_t>(batch_int8 >> shift) & 0xffffu;
+        skip_mask = static_cast<std::uint32_t>(batch_skip >> shift) & 0xffffu;
     };
 
     // ------------------------------------------------------ tile movement
