@@ -258,16 +258,20 @@ __device__ __forceinline__ void set_priority() {
 
 // Workgroup index -> (head, row group). Workgroups are dealt round-robin to
 // the XCDs; all row groups of a head run on one XCD so that its K / V / K8
-// stay in that XCD's L2. Causal problems start the heaviest (last) row
-// groups first, head after head, to shorten the tail.
+// stay in that XCD's L2. Causal problems take an XCD's heads four at a time
+// (fewer heads' K / V live in its L2 at once) and start the heaviest (last)
+// row groups of those heads first, head after head, to shorten the tail.
 __device__ __forceinline__ void map_block(int linear, int heads, int groups, bool causal, int& head, int& group) {
     int slot_group;
     if (heads % kXcds == 0) {
         const int xcd = linear % kXcds, slot = linear / kXcds;
         const int heads_per_xcd = heads / kXcds;
         if (causal) {
-            head = xcd + kXcds * (slot % heads_per_xcd);
-            slot_group = slot / heads_per_xcd;
+            const int batch_heads = heads_per_xcd % 4 == 0 ? 4 : heads_per_xcd;
+            const int per_batch = batch_heads * groups;
+            const int batch = slot / per_batch, r = slot % per_batch;
+            head = xcd + kXcds * (batch * batch_heads + r % batch_heads);
+            slot_group = r / batch_heads;
         } else {
             head = xcd + kXcds * (slot / groups);
             slot_group = slot % groups;
