@@ -65,6 +65,11 @@ def parse_args():
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="after timing, run one device copy of this many MiB on the bench stream "
                         "(calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE against known bytes)")
+    p.add_argument("--per-head", choices=["demo", "config"], default=None,
+                   help="time the drop-in per-head API (launch_fused_fp16_attention, precise P.V) instead: "
+                        "'demo' = the reference demo workload (M=1000 N=1003 d=128, g=2, mask 0xaaaa...), "
+                        "'config' = a loop of per-head calls over --config's heads (no causal mask or "
+                        "skip in that API: every pair is computed, skipped cells as FP16)")
     return p.parse_args()
 
 
@@ -88,6 +93,9 @@ def main() -> int:
         print(json.dumps({"error": "no GPU visible"}))
         return 1
     torch.cuda.set_device(0)
+    if args.per_head:
+        print(json.dumps(per_head_bench(args)), flush=True)
+        return 0
     w = workloads.WORKLOADS[args.config]
     log(w.describe())
     Q, K, V = workloads.make_inputs(w, args.seed)
@@ -195,7 +203,9 @@ def main() -> int:
     }
 
     measured = measured_traffic(w.describe())
-    if measured is not None:
+    if measured is not None and "stale" in measured:
+        result["roofline"]["traffic_stale"] = measured["stale"]
+    elif measured is not None:
         result["roofline"]["traffic"] = measured["traffic_bytes"]
         result["roofline"]["achieved_hbm_gbs"] = round(measured["traffic_bytes"] / (attn_ms * 1e-3) / 1e9, 1)
         result["roofline"]["traffic_source"] = measured["source"]
@@ -212,14 +222,121 @@ def main() -> int:
     return 0
 
 
+def per_head_bench(args) -> dict:
+    """The reference's own call pattern (src/main.cu:55-58, src/tests/tilemix_test.cu:487-500):
+    quantize_tilemix_qk, then launch_fused_fp16_attention with a TileMixRouting mask, one head
+    per call, precise (split fp16) P.V. Timed with HIP events over `steps` rounds on one
+    stream; a round is one quantize + one attention call per head."""
+    import torch
+    import tilemix
+    from tilemix import routing, workloads
+
+    dev = "cuda:0"
+    if args.per_head == "demo":
+        # src/main.cu:22-58: M=1000, N=1003, d=128, key_tiles_per_group 2, every routing word
+        # 0xaaaa... (odd 64-key groups INT8, even ones FP16), inputs periodic in the index.
+        M, N, d, g, heads = 1000, 1003, 128, 2, 1
+        # The demo's periodic inputs (periods 17, 19, 23; examples/demo_main.cpp).
+        idx = torch.arange(max(M, N) * d, dtype=torch.int64)
+        Q = (0.125 * ((idx[: M * d] % 17) - 8).float()).to(torch.float16).reshape(1, M, d).to(dev)
+        K = (0.125 * ((idx[: N * d] % 19) - 9).float()).to(torch.float16).reshape(1, N, d).to(dev)
+        V = (0.1 * ((idx[: N * d] % 23) - 11).float()).to(torch.float16).reshape(1, N, d).to(dev)
+        words = np.full(tilemix.routing_word_count(M, N, g), 0xAAAAAAAAAAAAAAAA, dtype=np.uint64)
+        route = torch.from_numpy(words.view(np.int64)).to(dev).reshape(1, -1)
+        kt = np.arange((N + 31) // 32)
+        codes = np.repeat(((kt // g) % 2 == 1).astype(np.uint8)[None, :], (M + 15) // 16, axis=0)[None]
+        name, scale = "reference demo (src/main.cu): M=1000 N=1003 d=128, g=2, mask 0xaaaa...", 1.0 / np.sqrt(d)
+        causal = False
+    else:
+        w = workloads.WORKLOADS[args.config]
+        Q, K, V = workloads.make_inputs(w, args.seed)
+        codes = workloads.make_codes(w, args.seed, Q, K)
+        codes = np.where(codes == routing.SKIP, routing.FP16, codes).astype(np.uint8)
+        route_np, _ = workloads.pack_heads(codes, w.key_tiles_per_group)
+        heads, M, N, d, g = w.heads, w.S, w.S, w.D, w.key_tiles_per_group
+        route = torch.from_numpy(route_np.view(np.int64)).to(dev).reshape(heads, -1)
+        name = (f"per-head loop over {w.describe()} as {heads} calls of the per-head API "
+                "(non-causal, skipped cells FP16)")
+        scale, causal = w.score_scale, False
+    O = torch.empty((heads, M, d), dtype=torch.float32, device=dev)
+    Q8 = torch.empty((heads, M, d), dtype=torch.int8, device=dev)
+    K8 = torch.empty((heads, N, d), dtype=torch.int8, device=dev)
+    qs = torch.empty((heads, (M + 127) // 128), dtype=torch.int16, device=dev)
+    ks = torch.empty((heads, (N + 63) // 64), dtype=torch.int16, device=dev)
+    stream = torch.cuda.Stream()
+    words_per_head = route.shape[1]
+
+    def one_round():
+        for h in range(heads):
+            tilemix.check(tilemix.quantize_tilemix_qk(Q[h], K[h], Q8[h], K8[h], qs[h], ks[h], M, N, d, stream),
+                          "quantize_tilemix_qk")
+            tilemix.check(tilemix.launch_fused_fp16_attention(
+                Q[h], K[h], V[h], O[h], M, N, d, float(scale), stream,
+                tilemix.TileMixRouting(route[h], words_per_head, g),
+                tilemix.TileMixQuantized(Q8[h], K8[h], qs[h], ks[h])), "launch_fused_fp16_attention")
+
+    with torch.cuda.stream(stream):
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < args.min_warmup_ms:
+            one_round()
+            torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(args.steps):
+            one_round()
+        end.record(stream)
+        torch.cuda.synchronize()
+    ms_per_round = start.elapsed_time(end) / args.steps
+    work = {"ops_int8": 0, "flops_fp16": 0}
+    for h in range(codes.shape[0]):
+        one = routing.algorithmic_work(codes[h], M, N, d, causal)
+        work["ops_int8"] += one["ops_int8"]
+        work["flops_fp16"] += one["flops_fp16"]
+    ops_total = work["ops_int8"] + work["flops_fp16"]
+    t_min = work["ops_int8"] / (PEAK_INT8_TOPS * 1e12) + work["flops_fp16"] / (PEAK_FP16_TFLOPS * 1e12)
+    achieved = ops_total / (ms_per_round * 1e-3) / 1e12
+    return {"metric": "per-head API effective TFLOP/s (quantize_tilemix_qk + launch_fused_fp16_attention)",
+            "value": round(achieved, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+            "ms_per_round": round(ms_per_round, 5), "calls_per_round": 2 * heads,
+            "higher_is_better": True, "dtype": "i8+f16 (i32/f32 accumulate), precise P.V",
+            "config": {"workload": name, "heads": heads, "M": M, "N": N, "d": d, "key_tiles_per_group": g},
+            "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                         "peak": round(ops_total / t_min / 1e12, 3), "unit": "TFLOP/s",
+                         "frac": round(t_min / (ms_per_round * 1e-3), 4),
+                         "note": "time per round includes the quantizer launches"}}
+
+
+# Sources whose change invalidates a recorded traffic measurement.
+STAMPED_SOURCES = ["tilemix-cuda_amd/csrc/attention.hip", "tilemix-cuda_amd/csrc/attention_common.h",
+                   "tilemix-cuda_amd/csrc/tilemix_device.h", "tilemix-cuda_amd/csrc/tilemix_launch.h",
+                   "tilemix-cuda_amd/csrc/quantize.hip", "tilemix-cuda_amd/build.py"]
+
+
+def source_stamp() -> str:
+    """First 16 hex digits of a SHA-256 over the kernel sources and build flags."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in STAMPED_SOURCES:
+        h.update(name.encode() + b"\0" + (ROOT / name).read_bytes() + b"\0")
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(workload: str):
     """HBM bytes per attention launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE
-    (calibrated on a copy of known size) for this workload, if recorded."""
+    (calibrated on a copy of known size) for this workload, if recorded for the
+    sources being run; {"stale": ...} when it was measured on other sources."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
         return None
     entry = json.loads(path.read_text()).get("attention_kernel")
-    return entry if entry and entry.get("workload") == workload else None
+    if not entry or entry.get("workload") != workload:
+        return None
+    current = source_stamp()
+    if entry.get("source_stamp") != current:
+        return {"stale": f"profiled sources {entry.get('source_stamp')} differ from these sources {current}; "
+                         "re-run the FETCH_SIZE / WRITE_SIZE passes"}
+    return entry
 
 
 def parity_check(w, Q, K, V, O, K8, k_scales, codes, args) -> dict:
