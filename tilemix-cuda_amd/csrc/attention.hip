@@ -7,20 +7,24 @@
 //    Q quantization block - and streams the keys in 64-key tiles, one K
 //    quantization block each, so q_scale is constant per workgroup and
 //    k_scale per tile.
-//  * Each wave owns 32 query rows (two 16-row routing cells tall). Scores are
-//    computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_f16 (FP16
-//    cells) or v_mfma_i32_16x16x64_i8 (INT8 cells, exact int32 dots). In that
-//    layout lane (g, i) holds four consecutive keys of query row i, so the
-//    online-softmax state of a row lives in lanes i, i+16, i+32, i+48 and
-//    needs only two cross-lane steps.
+//  * Each wave owns 32 query rows (two 16-row routing cells tall) and works
+//    on 32x32 MFMA blocks. Scores are computed transposed, S^T = K Q^T, with
+//    v_mfma_f32_32x32x16_f16 (FP16 cells) or v_mfma_i32_32x32x32_i8 (INT8
+//    cells, exact int32 dots), one block per 32 keys. In that layout lane
+//    (q, h) = (lane % 32, lane / 32) holds 16 keys of query row q, so a row's
+//    online-softmax state lives in lanes q and q + 32 and its maximum needs
+//    one cross-lane step. A 32x32 MFMA does the work of two 16x16 ones but
+//    holds the wave's instruction issue about as long as one, which leaves
+//    the SIMD free for the other wave's (or this wave's) VALU work.
 //  * The probabilities stay in registers and feed O^T += V^T P^T on
-//    v_mfma_f32_16x16x32_f16; the V^T operand is read from the row-major V
-//    tile in LDS with ds_read_b64_tr_b16, which transposes 16-bit elements
-//    across each 16-lane group. Key order inside a 32-key MFMA step is
-//    permuted identically on both operands. Row sums are the same MFMA with
-//    a block of ones in place of V^T (ones^T P^T): they add exactly the fp16
-//    probabilities P.V uses, over all of the row's keys, on the matrix core
-//    instead of the VALU.
+//    v_mfma_f32_32x32x16_f16: the accumulator elements of 8 consecutive
+//    score slots are exactly the P^T operand of one 16-key step, and the V^T
+//    operand is read from the row-major V tile in LDS with
+//    ds_read_b64_tr_b16, which transposes 16-bit elements across each
+//    16-lane group (key order inside a step permuted identically on both
+//    operands). Row sums add exactly the fp16 probabilities P.V uses
+//    (v_dot2_f32_f16 against ones); the two lanes of a row are summed once,
+//    at the end.
 //  * K, K8 and V tiles move HBM -> LDS with buffer_load ... lds (no VGPR
 //    staging): per-lane offsets into the LDS rows (unpadded with rotated
 //    16-byte chunks: all K8 rows, K / V rows of 128 or 256 bytes) are
@@ -37,8 +41,10 @@
 //    in the second, so of two waves in the same phase the one further along
 //    wins arbitration and leaves it first: this pushes the pair apart, one
 //    on the matrix core while the other runs exponentials.
-//  * A 16x32 routing cell covers whole 16x16 MFMA blocks, so each route is
-//    uniform per MFMA and the branch is taken on wave-uniform route masks.
+//  * A 32-key MFMA block is one routing cell wide and two cells (the wave's
+//    two 16-row halves) tall. The branch is taken on wave-uniform route
+//    masks; a wave whose cells mix routes computes both score kinds and
+//    selects per lane.
 //  * The optional in-kernel Q quantization reproduces quantize_tilemix_qk's
 //    bytes exactly: the workgroup's 128 rows are exactly one Q block.
 
@@ -67,15 +73,12 @@ struct Layout {
     static constexpr int kDP = 32 * DC;            // padded head dim, fp16 path
     static constexpr int kD8C = (DC + 1) / 2;      // 64-feature chunks, int8 path
     static constexpr int kDP8 = 64 * kD8C;
-    static constexpr int kFB = kDP / 16;           // 16-feature output blocks
     // K / V rows hold 2 * kDP bytes. Rows of 256 bytes (d > 96) and 128 bytes
     // (32 < d <= 64) are unpadded, with 16-byte chunk c of row r at chunk
-    // position (c + rot(r)) mod (chunks per row), rot(r) = 2r mod 16 on
-    // 256-byte rows and r & 6 on 128-byte rows: the bank pattern of a 32-byte
-    // pad, under which the K fragment and transposed V reads are
-    // conflict-free, with no pad bytes to move. Other rows are padded by 16 (K)
-    // or 32 (V) bytes. K8 rows are 128 bytes (d > 64, r & 6 rotation) or 64
-    // bytes (2 * ((r >> 2) & 1), mod 4).
+    // position (c + rot(r)) mod (chunks per row), so that the fragment reads
+    // are free of LDS bank conflicts with no pad bytes to move (rot below).
+    // Other rows are padded by 16 (K) or 32 (V) bytes. K8 rows are 128 bytes
+    // (d > 64) or 64 bytes, rotated the same way.
     static constexpr int kRowBytes = kDP * 2;
     static constexpr bool kRotate = kRowBytes == 256 || kRowBytes == 128;
     static constexpr bool kRotate8 = kDP8 == 128 || kDP8 == 64;
@@ -97,115 +100,130 @@ struct Layout {
     static constexpr int kSmemBytes = kKBytes + kVBytes + kK8Bytes;
     static_assert(kKBytes % 1024 == 0 && kVBytes % 1024 == 0 && kK8Bytes % 1024 == 0,
                   "tiles are whole wave loads");
-    // Chunk rotation of a rotated row of kChunks 16-byte chunks.
-    template <int kChunks>
+    // Chunk rotation of a rotated row of kChunks 16-byte chunks. Key rows
+    // (K, K8) are read as 32 consecutive rows x one chunk per half-wave:
+    // rotations that put every pair of such rows on its own bank group. Value
+    // rows are read by ds_read_b64_tr_b16 in 4-row x 16-feature blocks.
+    template <int kChunks, bool kKey>
     __device__ static int rot(int row) {
         static_assert(kChunks == 16 || kChunks == 8 || kChunks == 4, "rotated rows are 256, 128 or 64 bytes");
-        return kChunks == 16 ? (2 * row) & 15 : kChunks == 8 ? row & 6 : 2 * ((row >> 2) & 1);
+        if constexpr (kKey)
+            return kChunks == 16 ? row & 15 : kChunks == 8 ? (row >> 1) & 7 : ((row >> 1) ^ (row >> 3)) & 3;
+        else
+            return kChunks == 16 ? (2 * row) & 15 : kChunks == 8 ? row & 6 : 2 * ((row >> 2) & 1);
     }
     // Offset of byte `byte` of row `row` in a rotated tile.
-    template <int kChunks>
+    template <int kChunks, bool kKey>
     __device__ static int rotated(int row, int byte) {
-        return row * 16 * kChunks + ((((byte >> 4) + rot<kChunks>(row)) & (kChunks - 1)) << 4) + (byte & 15);
+        return row * 16 * kChunks + ((((byte >> 4) + rot<kChunks, kKey>(row)) & (kChunks - 1)) << 4) + (byte & 15);
     }
     // Global offset that DMA lane `lane` of 1 KiB piece w fetches for a
     // rotated tile (kOutOfRange past the row's bytes): the inverse of rotated.
-    template <int kChunks>
+    template <int kChunks, bool kKey>
     __device__ static int rotated_lane(int w, int lane, int row_bytes, int global_row_bytes) {
         const int landing = 1024 * w + 16 * lane;
         const int row = landing / (16 * kChunks);
-        const int column = ((((landing >> 4) & (kChunks - 1)) - rot<kChunks>(row)) & (kChunks - 1)) << 4;
+        const int column = ((((landing >> 4) & (kChunks - 1)) - rot<kChunks, kKey>(row)) & (kChunks - 1)) << 4;
         return column < row_bytes ? row * global_row_bytes + column : kOutOfRange;
     }
     // Offset of byte `byte` (< 2 * kDP, or < kDP8 for K8) of row `row` in the
     // K / V / K8 tile.
     __device__ static int k_at(int row, int byte) {
-        if constexpr (kRotate) return rotated<kRowBytes / 16>(row, byte);
+        if constexpr (kRotate) return rotated<kRowBytes / 16, true>(row, byte);
         else return row * kKStride + byte;
     }
     __device__ static int v_at(int row, int byte) {
-        if constexpr (kRotate) return rotated<kRowBytes / 16>(row, byte);
+        if constexpr (kRotate) return rotated<kRowBytes / 16, false>(row, byte);
         else return row * kVStride + byte;
     }
     __device__ static int k8_at(int row, int byte) {
-        if constexpr (kRotate8) return rotated<kDP8 / 16>(row, byte);
+        if constexpr (kRotate8) return rotated<kDP8 / 16, true>(row, byte);
         else return row * kK8Stride + byte;
     }
     // Global offset that DMA lane `lane` of 1 KiB piece w fetches.
+    template <bool kKey>
     __device__ static int kv_lane_offset(int w, int lane, int stride, int row_bytes, int global_row_bytes) {
-        if constexpr (kRotate) return rotated_lane<kRowBytes / 16>(w, lane, row_bytes, global_row_bytes);
+        if constexpr (kRotate) return rotated_lane<kRowBytes / 16, kKey>(w, lane, row_bytes, global_row_bytes);
         else return lane_offset(w, lane, stride, row_bytes, global_row_bytes);
     }
     __device__ static int k8_lane_offset(int w, int lane, int row_bytes) {
-        if constexpr (kRotate8) return rotated_lane<kDP8 / 16>(w, lane, row_bytes, row_bytes);
+        if constexpr (kRotate8) return rotated_lane<kDP8 / 16, true>(w, lane, row_bytes, row_bytes);
         else return lane_offset(w, lane, kK8Stride, row_bytes, row_bytes);
     }
 };
 
-// Online-softmax state of the two 16-row query blocks a wave owns (scores in
-// the log2 domain, m raised lazily; see kLazyRescale).
-template <int kFB>
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef int int16v __attribute__((ext_vector_type(16)));
+
+// Online-softmax state of the query row a lane owns (row lane & 31 of the
+// wave's 32; lanes l and l ^ 32 hold the same row, each for half of every
+// 32-key block), scores in the log2 domain, m raised lazily (kLazyRescale).
+template <int kOB>
 struct RowState {
-    float4v o[2][kFB];  // O^T accumulators: lane (g, i) holds O[row i][16fb + 4g + r]
-    float4v l[2];       // row sums of P (ones^T P^T): every element holds row i's sum
-    float m[2];
+    // O^T accumulators: o[fb][j] is output row R = 8 (j / 4) + 4 h + j % 4
+    // (h = lane / 32) of feature block fb, i.e. feature 16 fb + R for R < 16
+    // and kDP / 2 + 16 fb + R - 16 above (the two 16-row halves of a block
+    // sit kDP / 2 features apart, which keeps the transposed V reads free of
+    // bank conflicts).
+    float16v o[kOB];
+    float lsum;       // this lane's part of the row sum of P (the fp16 values P.V uses)
+    float m;
 };
 
-// x[b][kb] holds the 16 scores of query row i of block b for keys
-// 16kb + 4g + r; c is the per-tile log2-domain factor (>= 0); explicit scores
-// pass c = 1. Both blocks of the wave are handled together: each lane's
-// maximum of its 16 scores, one wave-uniform branch for the rare rescale, and
-// there one pass of row maxima (the cross-lane steps of the two blocks
-// interleave).
-template <int kFB, bool kPrecise>
-__device__ __forceinline__ void softmax_tile(RowState<kFB>& st, const float4v (&x)[2][4], float c,
-                                             half8 (&ph)[2][2], half8 (&pl)[2][2]) {
-    float tile[2];
+// Maximum of the 16 values of a 32x32 accumulator block, 8 v_max3.
+__device__ __forceinline__ float block_max16(const float16v& x) {
+    const float a = max3(x[0], x[1], x[2]), b = max3(x[3], x[4], x[5]), e = max3(x[6], x[7], x[8]);
+    const float f = max3(x[9], x[10], x[11]), g = max3(x[12], x[13], x[14]);
+    return max3(max3(a, b, e), max3(f, g, x[15]), x[15]);
+}
+
+// x[kb][j] holds the score of the lane's row against key 32 kb + 8 (j / 4) +
+// 4 h + j % 4; c is the per-tile log2-domain factor (>= 0; explicit scores
+// pass c = 1). ph[ks] / pl[ks] receive the fp16 probabilities of keys
+// 16 ks + {4h .. 4h + 3, 8 + 4h .. 8 + 4h + 3}: the B operand (P^T) of the
+// 32x32x16 P.V MFMA for key step ks.
+template <int kOB, bool kPrecise>
+__device__ __forceinline__ void softmax_tile(RowState<kOB>& st, const float16v (&x)[2], float c,
+                                             half8 (&ph)[4], half8 (&pl)[4]) {
+    const float tile = max3(block_max16(x[0]), block_max16(x[1]), block_max16(x[1])) * c;  // c >= 0
+    // The row's maximum exceeds m + kLazyRescale exactly when one of its two
+    // lanes' own maxima does.
+    if (__any(tile > st.m + kLazyRescale)) {
+        float a = tile, b = tile;
+        permlane32_swap(a, b);
+        const float m_new = fmaxf(st.m, max3(a, b, b));
+        // Rows with no visible key yet keep m = -inf (their sums are still 0).
+        const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(st.m - m_new);
+        st.m = m_new;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const float t0 = max3(max3(x[b][0][0], x[b][0][1], x[b][0][2]), x[b][0][3], x[b][1][3]);
-        const float t1 = max3(x[b][1][0], x[b][1][1], x[b][1][2]);
-        const float t2 = max3(max3(x[b][2][0], x[b][2][1], x[b][2][2]), x[b][2][3], x[b][3][3]);
-        const float t3 = max3(x[b][3][0], x[b][3][1], x[b][3][2]);
-        tile[b] = max3(max3(t0, t1, t2), t3, t3) * c;  // c >= 0: max(x) * c == max(x * c)
+        for (int fb = 0; fb < kOB; ++fb) st.o[fb] *= alpha;
+        st.lsum *= alpha;
     }
-    // A row's maximum exceeds m + kLazyRescale exactly when one of its four
-    // lanes' own maxima does, so the row maxima (two cross-lane steps) are
-    // formed only on the rare tiles that raise the running maximum.
-    const bool raise0 = tile[0] > st.m[0] + kLazyRescale, raise1 = tile[1] > st.m[1] + kLazyRescale;
-    if (__any(raise0 || raise1)) {
-        row_max4_pair(tile[0], tile[1]);
+    // m == -inf only while every score seen, this tile included, is masked.
+    const float neg_m = st.m == -INFINITY ? 0.0f : -st.m;
+    const half2v ones{1.0f16, 1.0f16};
+    float part[4];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            // Rows with no visible key yet keep m = -inf (their sums are still 0).
-            const float m_new = fmaxf(st.m[b], tile[b]);
-            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(st.m[b] - m_new);
-            st.m[b] = m_new;
+    for (int ks = 0; ks < 4; ++ks) {
+        const int kb = ks >> 1, base = 8 * (ks & 1);
 #pragma unroll
-            for (int fb = 0; fb < kFB; ++fb) st.o[b][fb] *= alpha;
-            st.l[b] *= alpha;
+        for (int e = 0; e < 8; ++e) {
+            const float v = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kb][base + e], c, neg_m));
+            const _Float16 hv = static_cast<_Float16>(v);
+            ph[ks][e] = hv;
+            if constexpr (kPrecise) pl[ks][e] = static_cast<_Float16>(v - static_cast<float>(hv));
         }
+        // Row sums of exactly the fp16 values the P.V MFMAs use.
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            sum = __builtin_amdgcn_fdot2(half2v{ph[ks][e], ph[ks][e + 1]}, ones, sum, false);
+            if constexpr (kPrecise) sum = __builtin_amdgcn_fdot2(half2v{pl[ks][e], pl[ks][e + 1]}, ones, sum, false);
+        }
+        part[ks] = sum;
+        if (ks == 1) set_priority<2>();  // second half of the VALU phase
     }
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        // m == -inf only while every score seen, this tile included, is masked.
-        const float neg_m = st.m[b] == -INFINITY ? 0.0f : -st.m[b];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float a = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][2 * ks][r], c, neg_m));
-                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(x[b][2 * ks + 1][r], c, neg_m));
-                const _Float16 ha = static_cast<_Float16>(a), he = static_cast<_Float16>(e);
-                ph[b][ks][r] = ha;
-                ph[b][ks][4 + r] = he;
-                if constexpr (kPrecise) {
-                    pl[b][ks][r] = static_cast<_Float16>(a - static_cast<float>(ha));
-                    pl[b][ks][4 + r] = static_cast<_Float16>(e - static_cast<float>(he));
-                }
-            }
-        if (b == 0) set_priority<2>();  // second half of the VALU phase
-    }
+    st.lsum += (part[0] + part[1]) + (part[2] + part[3]);
 }
 
 // load_to_lds with M0 = lds_address + kOffset, the add issued inside the asm
@@ -241,8 +259,9 @@ template <int DC, bool kVector, bool kPrecise, bool kDots>
 __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kernel(const AttnParams p) {
     using L = Layout<DC>;
     constexpr int kDP = L::kDP;
-    constexpr int kD8C = L::kD8C;
-    constexpr int kFB = L::kFB;
+    constexpr int kOB = DC;               // 32-feature output blocks
+    constexpr int kQC = kDP / 16;         // 16-feature Q / K chunks (fp16 MFMA k-steps)
+    constexpr int kQ8C = L::kDP8 / 32;    // 32-feature Q8 / K8 chunks (int8 MFMA k-steps)
     __shared__ __attribute__((aligned(16))) unsigned char smem[L::kSmemBytes];
     // Quantized Q rows (B operand of the INT8 MFMA), read on INT8 tiles only.
     __shared__ __attribute__((aligned(16))) unsigned char lds_q8[L::kQ8Bytes];
@@ -260,8 +279,9 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane >> 4;
     const int i = lane & 15;
+    const int q = lane & 31;  // the lane's query row within the wave (and its MFMA column)
+    const int h = lane >> 5;  // which half of each 32-key / 16-feature block the lane holds
 
     int head32, qblock;
     map_block(blockIdx.x, p.heads, p.q_blocks, p.causal != 0, head32, qblock);
@@ -277,21 +297,22 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     unsigned char* const Oh = static_cast<unsigned char*>(p.O) + head * p.o_stride * (p.o_dtype == TILEMIX_DTYPE_F32 ? 4 : 2);
 
     // ---------------------------------------------------------------- Q
-    half8 qf[2][DC];
+    // B operand of the 32x32x16 QK^T MFMA: lane (q, h) holds features
+    // 16c + 8h .. 16c + 8h + 7 of its row for chunk c.
+    half8 qf[kQC];
+    {
+        const int row = qw + q;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const int row = qw + 16 * b + i;
-#pragma unroll
-        for (int dc = 0; dc < DC; ++dc) {
-            const int feature = 32 * dc + 8 * g;
+        for (int c = 0; c < kQC; ++c) {
+            const int feature = 16 * c + 8 * h;
             if constexpr (kVector) {
-                qf[b][dc] = (row < M && feature < d)
+                qf[c] = (row < M && feature < d)
                     ? *reinterpret_cast<const half8*>(Qh + static_cast<std::int64_t>(row) * p.q_row + feature)
                     : half8{};
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    qf[b][dc][e] = (row < M && feature + e < d)
+                    qf[c][e] = (row < M && feature + e < d)
                         ? __builtin_bit_cast(_Float16, Qh[static_cast<std::int64_t>(row) * p.q_row + feature + e])
                         : static_cast<_Float16>(0.0f);
             }
@@ -306,13 +327,11 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             // for them, NaN patterns (> 0x7c00) sorting above +inf.
             unsigned top = 0;
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+            for (int c = 0; c < kQC; ++c) {
+                const uint4v words = __builtin_bit_cast(uint4v, qf[c]);
 #pragma unroll
-                for (int dc = 0; dc < DC; ++dc) {
-                    const uint4v words = __builtin_bit_cast(uint4v, qf[b][dc]);
-#pragma unroll
-                    for (int w = 0; w < 4; ++w) top = max_u16x2(top, words[w] & 0x7fff7fffu);
-                }
+                for (int w = 0; w < 4; ++w) top = max_u16x2(top, words[w] & 0x7fff7fffu);
+            }
             unsigned bits = wave_max_bits(max(top & 0xffffu, top >> 16));
             if (lane == 0) group_bits[wave] = bits;
             __syncthreads();
@@ -321,18 +340,16 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 // A NaN in the block: the maximum skips NaNs, as fmaxf does.
                 unsigned clean = 0;
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
+                for (int c = 0; c < kQC; ++c)
 #pragma unroll
-                    for (int dc = 0; dc < DC; ++dc)
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            // The element is copied out first: __builtin_bit_cast
-                            // applied to a vector element expression reads
-                            // element 0 under this compiler.
-                            const _Float16 x = qf[b][dc][e];
-                            const unsigned h = __builtin_bit_cast(std::uint16_t, x) & 0x7fffu;
-                            clean = h <= 0x7c00u ? max(clean, h) : clean;
-                        }
+                    for (int e = 0; e < 8; ++e) {
+                        // The element is copied out first: __builtin_bit_cast
+                        // applied to a vector element expression reads
+                        // element 0 under this compiler.
+                        const _Float16 x = qf[c][e];
+                        const unsigned hb = __builtin_bit_cast(std::uint16_t, x) & 0x7fffu;
+                        clean = hb <= 0x7c00u ? max(clean, hb) : clean;
+                    }
                 clean = wave_max_bits(clean);
                 __syncthreads();
                 if (lane == 0) group_bits[wave] = clean;
@@ -345,15 +362,14 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             q_scale = static_cast<float>(stored);
             if (tid == 0 && p.q_scales_out)
                 p.q_scales_out[head * p.q_blocks + qblock] = __builtin_bit_cast(std::uint16_t, stored);
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                const int local = wave * kRowsPerWave + 16 * b + i;
+            {
+                const int local = wave * kRowsPerWave + q;
                 const int row = q0 + local;
 #pragma unroll
-                for (int dc = 0; dc < 2 * kD8C; ++dc) {
+                for (int c = 0; c < L::kDP8 / 16; ++c) {
                     uint2v packed{0u, 0u};
-                    if (dc < DC && scale > 0.0f) {
-                        const uint4v words = __builtin_bit_cast(uint4v, qf[b][dc < DC ? dc : 0]);
+                    if (c < kQC && scale > 0.0f) {
+                        const uint4v words = __builtin_bit_cast(uint4v, qf[c < kQC ? c : 0]);
                         int v[8];
 #pragma unroll
                         for (int w = 0; w < 4; ++w) {
@@ -363,7 +379,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                         packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
                         packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);
                     }
-                    const int feature = 32 * dc + 8 * g;
+                    const int feature = 16 * c + 8 * h;
                     *reinterpret_cast<uint2v*>(lds_q8 + local * L::kQ8Stride + feature) = packed;
                     if (p.q8_out && row < M && feature < d) {
                         std::int8_t* dst = p.q8_out + head * static_cast<std::int64_t>(M) * d +
@@ -380,29 +396,26 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         } else {
             q_scale = half_bits_to_float(p.q_scales[head * p.q_blocks + qblock]);
             const std::int8_t* Q8h = p.Q8 + head * static_cast<std::int64_t>(M) * d;
+            const int local = wave * kRowsPerWave + q;
+            const int row = q0 + local;
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                const int local = wave * kRowsPerWave + 16 * b + i;
-                const int row = q0 + local;
+            for (int m = 0; m < kQ8C; ++m) {
+                const int feature = 32 * m + 16 * h;
+                int4v chunk;
+                if constexpr (kVector) {
+                    chunk = (row < M && feature < d)
+                        ? *reinterpret_cast<const int4v*>(Q8h + static_cast<std::int64_t>(row) * d + feature)
+                        : int4v{0, 0, 0, 0};
+                } else {
+                    unsigned char bytes[16];
 #pragma unroll
-                for (int m = 0; m < kD8C; ++m) {
-                    const int feature = 64 * m + 16 * g;
-                    int4v chunk;
-                    if constexpr (kVector) {
-                        chunk = (row < M && feature < d)
-                            ? *reinterpret_cast<const int4v*>(Q8h + static_cast<std::int64_t>(row) * d + feature)
-                            : int4v{0, 0, 0, 0};
-                    } else {
-                        unsigned char bytes[16];
-#pragma unroll
-                        for (int e = 0; e < 16; ++e)
-                            bytes[e] = (row < M && feature + e < d)
-                                ? static_cast<unsigned char>(Q8h[static_cast<std::int64_t>(row) * d + feature + e])
-                                : 0;
-                        chunk = __builtin_bit_cast(int4v, bytes);
-                    }
-                    *reinterpret_cast<int4v*>(lds_q8 + local * L::kQ8Stride + feature) = chunk;
+                    for (int e = 0; e < 16; ++e)
+                        bytes[e] = (row < M && feature + e < d)
+                            ? static_cast<unsigned char>(Q8h[static_cast<std::int64_t>(row) * d + feature + e])
+                            : 0;
+                    chunk = __builtin_bit_cast(int4v, bytes);
                 }
+                *reinterpret_cast<int4v*>(lds_q8 + local * L::kQ8Stride + feature) = chunk;
             }
         }
         __syncthreads();  // lds_q8 complete
@@ -469,13 +482,13 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 #pragma unroll
         for (int t = 0; t < L::kKPerWave; ++t) {
             const int w = wave + kWavesPerGroup * t;
-            off_k[t] = w < L::kKLoads ? L::kv_lane_offset(w, lane, L::kKStride, 2 * d, k_row_bytes) : kOutOfRange;
+            off_k[t] = w < L::kKLoads ? L::template kv_lane_offset<true>(w, lane, L::kKStride, 2 * d, k_row_bytes) : kOutOfRange;
             dst_k[t] = w < L::kKLoads ? lds_k_address + 1024 * w : lds_spare_address;
         }
 #pragma unroll
         for (int t = 0; t < L::kVPerWave; ++t) {
             const int w = wave + kWavesPerGroup * t;
-            off_v[t] = w < L::kVLoads ? L::kv_lane_offset(w, lane, L::kVStride, 2 * d, v_row_bytes) : kOutOfRange;
+            off_v[t] = w < L::kVLoads ? L::template kv_lane_offset<false>(w, lane, L::kVStride, 2 * d, v_row_bytes) : kOutOfRange;
             dst_v[t] = w < L::kVLoads ? lds_v_address + 1024 * w : lds_spare_address;
         }
 #pragma unroll
@@ -563,36 +576,35 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     };
 
     // The wave's quantized Q rows (INT8 operand), kept in registers.
-    int4v q8f[2][kD8C];
+    int4v q8f[kQ8C];
     if (p.int8_operands) {
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int m = 0; m < kD8C; ++m)
-                q8f[b][m] = *reinterpret_cast<const int4v*>(
-                    lds_q8 + (wave * kRowsPerWave + 16 * b + i) * L::kQ8Stride + 64 * m + 16 * g);
+        for (int m = 0; m < kQ8C; ++m)
+            q8f[m] = *reinterpret_cast<const int4v*>(lds_q8 + (wave * kRowsPerWave + q) * L::kQ8Stride + 32 * m + 16 * h);
     }
     // Per-lane LDS offsets of the K fragment (feature chunk dc, key block 0)
     // and V^T fragment (feature block fb, key step 0) reads; key blocks and
     // steps add whole rows (multiples of 16, which keep the chunk rotation).
-    int k_lane[DC], v_lane[kFB], k8_lane[kD8C];
+    // K / K8 fragments: lane (q, h) reads key q of the key block, 16 bytes
+    // at feature chunk c. V^T fragments (ds_read_b64_tr_b16): the 16-lane
+    // group (fh, h) = ((lane / 16) & 1, lane / 32) reads keys 4h .. 4h + 3
+    // (then 8 + 4h ..) x features 16 fb + fh kDP / 2 .. + 15, lane i
+    // receiving feature 16 fb + fh kDP / 2 + i (output row 16 fh + i).
+    int k_lane[kQC], v_lane[kOB], k8_lane[kQ8C];
 #pragma unroll
-    for (int m = 0; m < kD8C; ++m) k8_lane[m] = L::k8_at(i, 64 * m + 16 * g);
+    for (int m = 0; m < kQ8C; ++m) k8_lane[m] = L::k8_at(q, 32 * m + 16 * h);
 #pragma unroll
-    for (int dc = 0; dc < DC; ++dc) k_lane[dc] = L::k_at(i, (32 * dc + 8 * g) * 2);
+    for (int c = 0; c < kQC; ++c) k_lane[c] = L::k_at(q, 32 * c + 16 * h);
 #pragma unroll
-    for (int fb = 0; fb < kFB; ++fb) v_lane[fb] = L::v_at(4 * g + (i >> 2), 8 * (i & 3) + 32 * fb);
+    for (int fb = 0; fb < kOB; ++fb)
+        v_lane[fb] = L::v_at(4 * h + (i >> 2), 2 * (16 * fb + (kDP / 2) * ((lane >> 4) & 1) + 4 * (i & 3)));
     // ---------------------------------------------------------- key loop
-    RowState<kFB> st;
+    RowState<kOB> st;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-        for (int fb = 0; fb < kFB; ++fb) st.o[b][fb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-        st.l[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-        st.m[b] = -INFINITY;
-    }
+    for (int fb = 0; fb < kOB; ++fb) st.o[fb] = float16v{};
+    st.lsum = 0.0f;
+    st.m = -INFINITY;
     const bool positive_scale = p.score_scale >= 0.0f;
-    const half8 ones{1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
 
     const int key_tiles64 = (N - 1) / kTileKeys + 1;
     int tiles = key_tiles64;
@@ -644,11 +656,11 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         const bool masked = k0 + kTileKeys > N || (p.causal && k0 + kTileKeys - 1 > qw);
         const bool fast = positive_scale && !masked;
 
-        float4v s[2][4];
+        float16v s[2];
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) s[b][kb] = float4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            for (int e = 0; e < 16; ++e) s[kb][e] = -INFINITY;
         float c = 1.0f;
         if (active) {
             float k_factor = 0.0f;  // q_scale * k_scale * score_scale * log2(e)
@@ -656,204 +668,154 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 const float k_scale = half_bits_to_float(load_uniform_u16(p.k_scales + head * p.k_blocks + j));
                 k_factor = ((q_scale * k_scale) * p.score_scale) * kLog2e;
             }
-            // ---- scores S^T[kb][b]: lane (g, i) holds query i, keys 16kb + 4g + r
+            // ---- scores S^T[kb]: lane (q, h) holds row q against keys 32 kb + 8 (e / 4) + 4 h + e % 4
             auto fp16_scores = [&]() {
-                // Feature chunk outermost (eight independent accumulator
-                // chains), the next chunk's K fragments read ahead.
+                // Feature chunk outermost (two independent accumulator
+                // chains), K fragments read two chunks ahead.
+                s[0] = float16v{};
+                s[1] = float16v{};
+                half8 kf[3][2];
+                auto load_c = [&](int cc, half8 (&dst)[2]) {
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb) s[b][kb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-                half8 kf[2][4];
-                auto load_dc = [&](int dc, half8 (&dst)[4]) {
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-                        dst[kb] = *reinterpret_cast<const half8*>(lds_k + 16 * L::kKStride * kb + k_lane[dc]);
+                    for (int kb = 0; kb < 2; ++kb)
+                        dst[kb] = *reinterpret_cast<const half8*>(lds_k + 32 * L::kKStride * kb + k_lane[cc]);
                 };
-                load_dc(0, kf[0]);
+                load_c(0, kf[0]);
+                load_c(1, kf[1]);
 #pragma unroll
-                for (int dc = 0; dc < DC; ++dc) {
-                    if (dc + 1 < DC) load_dc(dc + 1, kf[(dc + 1) & 1]);
+                for (int cc = 0; cc < kQC; ++cc) {
+                    if (cc + 2 < kQC) load_c(cc + 2, kf[(cc + 2) % 3]);
 #pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                        for (int b = 0; b < 2; ++b)
-                            s[b][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[dc & 1][kb], qf[b][dc], s[b][kb], 0, 0, 0);
+                    for (int kb = 0; kb < 2; ++kb)
+                        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[cc % 3][kb], qf[cc], s[kb], 0, 0, 0);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             };
-            // Exact int32 dots of key block kb for both query blocks.
-            auto int8_dots = [&](int kb, int4v& acc0, int4v& acc1) {
-                acc0 = int4v{0, 0, 0, 0};
-                acc1 = int4v{0, 0, 0, 0};
+            // Exact int32 dots of both key blocks.
+            auto int8_scores = [&](int16v (&acc)[2]) {
+                acc[0] = int16v{};
+                acc[1] = int16v{};
+                int4v kf8[2][2];
+                auto load_m = [&](int m, int4v (&dst)[2]) {
 #pragma unroll
-                for (int m = 0; m < kD8C; ++m) {
-                    const int4v kf = *reinterpret_cast<const int4v*>(
-                        lds_k8 + 16 * L::kK8Stride * kb + k8_lane[m]);
-                    acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, q8f[0][m], acc0, 0, 0, 0);
-                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, q8f[1][m], acc1, 0, 0, 0);
+                    for (int kb = 0; kb < 2; ++kb)
+                        dst[kb] = *reinterpret_cast<const int4v*>(lds_k8 + 32 * L::kK8Stride * kb + k8_lane[m]);
+                };
+                load_m(0, kf8[0]);
+#pragma unroll
+                for (int m = 0; m < kQ8C; ++m) {
+                    if (m + 1 < kQ8C) load_m(m + 1, kf8[(m + 1) & 1]);
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+                        acc[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf8[m & 1][kb], q8f[m], acc[kb], 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-                __builtin_amdgcn_sched_barrier(0);
             };
-            // Raw int32 dots of INT8 cells (verification output).
-            auto store_dots = [&](int kb, int b, const int4v& acc) {
-                const int query = qw + 16 * b + i;
+            // Raw int32 dots of key block kb (verification output).
+            auto store_dots = [&](int kb, const int16v& acc) {
+                const int query = qw + q;
                 std::int32_t* row = p.dots + head * static_cast<std::int64_t>(M) * N +
                                     static_cast<std::int64_t>(query) * N;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int key = k0 + 16 * kb + 4 * g + r;
-                    if (query < M && key < N && !(p.causal && key > query)) row[key] = acc[r];
+                for (int e = 0; e < 16; ++e) {
+                    const int key = k0 + 32 * kb + 8 * (e >> 2) + 4 * h + (e & 3);
+                    if (query < M && key < N && !(p.causal && key > query)) row[key] = acc[e];
                 }
             };
+            const int qh = q >> 4;  // the lane's 16-row routing cell of the wave
             if (wave_skip == 0 && wave_int8 == 0) {
                 fp16_scores();
                 c = p.score_log2;
             } else if (wave_skip == 0 && wave_int8 == 0xfu) {
-                int4v acc[2][4];
+                int16v acc[2];
+                int8_scores(acc);
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
+                for (int kb = 0; kb < 2; ++kb) {
+                    if (kDots && p.dots) store_dots(kb, acc[kb]);
 #pragma unroll
-                    for (int kb = 0; kb < 4; ++kb) acc[b][kb] = int4v{0, 0, 0, 0};
-                int4v kf8[2][4];
-                auto load_m = [&](int m, int4v (&dst)[4]) {
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-                        dst[kb] = *reinterpret_cast<const int4v*>(lds_k8 + 16 * L::kK8Stride * kb + k8_lane[m]);
-                };
-                load_m(0, kf8[0]);
-#pragma unroll
-                for (int m = 0; m < kD8C; ++m) {
-                    if (m + 1 < kD8C) load_m(m + 1, kf8[(m + 1) & 1]);
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                        for (int b = 0; b < 2; ++b)
-                            acc[b][kb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf8[m & 1][kb], q8f[b][m], acc[b][kb], 0, 0, 0);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                    if (kDots && p.dots) {
-                        store_dots(kb, 0, acc[0][kb]);
-                        store_dots(kb, 1, acc[1][kb]);
-                    }
-#pragma unroll
-                    for (int b = 0; b < 2; ++b)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) s[b][kb][r] = static_cast<float>(acc[b][kb][r]);
+                    for (int e = 0; e < 16; ++e) s[kb][e] = static_cast<float>(acc[kb][e]);
                 }
                 c = k_factor;
             } else {
                 // Mixed routes inside the wave: both score kinds where present,
-                // explicitly scaled, then selected per cell (bit 2b + kb/2).
+                // explicitly scaled, then selected per lane (cell bit 2 qh + kb).
                 const unsigned wave_fp16 = ~(wave_int8 | wave_skip) & 0xfu;
                 if (wave_fp16) {
                     fp16_scores();
 #pragma unroll
-                    for (int b = 0; b < 2; ++b)
-#pragma unroll
-                        for (int kb = 0; kb < 4; ++kb) s[b][kb] *= p.score_log2;
+                    for (int kb = 0; kb < 2; ++kb) s[kb] *= p.score_log2;
                 } else {
-#pragma unroll
-                    for (int b = 0; b < 2; ++b)
-#pragma unroll
-                        for (int kb = 0; kb < 4; ++kb) s[b][kb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+                    s[0] = float16v{};
+                    s[1] = float16v{};
                 }
                 if (wave_int8) {
+                    int16v acc[2];
+                    int8_scores(acc);
 #pragma unroll
-                    for (int kb = 0; kb < 4; ++kb) {
-                        int4v acc[2];
-                        int8_dots(kb, acc[0], acc[1]);
+                    for (int kb = 0; kb < 2; ++kb) {
+                        const bool cell_int8 = (wave_int8 >> (2 * qh + kb)) & 1u;
+                        if (kDots && p.dots && cell_int8) store_dots(kb, acc[kb]);
 #pragma unroll
-                        for (int b = 0; b < 2; ++b) {
-                            const bool cell_int8 = (wave_int8 >> (2 * b + (kb >> 1))) & 1u;
-                            if (kDots && p.dots && cell_int8) store_dots(kb, b, acc[b]);
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                s[b][kb][r] = cell_int8 ? static_cast<float>(acc[b][r]) * k_factor : s[b][kb][r];
-                        }
+                        for (int e = 0; e < 16; ++e)
+                            s[kb][e] = cell_int8 ? static_cast<float>(acc[kb][e]) * k_factor : s[kb][e];
                     }
                 }
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
+                for (int kb = 0; kb < 2; ++kb)
+                    if ((wave_skip >> (2 * qh + kb)) & 1u)
 #pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-                        if ((wave_skip >> (2 * b + (kb >> 1))) & 1u)
-                            s[b][kb] = float4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+                        for (int e = 0; e < 16; ++e) s[kb][e] = -INFINITY;
                 c = 1.0f;
             }
             if (!fast && c != 1.0f) {
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb) s[b][kb] *= c;
+                for (int kb = 0; kb < 2; ++kb) s[kb] *= c;
                 c = 1.0f;
             }
             // ---- element masks: key tail and causal diagonal (explicit scores)
             if (masked) {
+                const int query = qw + q;
 #pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const int query = qw + 16 * b + i;
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int key = k0 + 16 * kb + 4 * g + r;
-                            if (key >= N || (p.causal && key > query)) s[b][kb][r] = -INFINITY;
-                        }
-                }
+                    for (int e = 0; e < 16; ++e) {
+                        const int key = k0 + 32 * kb + 8 * (e >> 2) + 4 * h + (e & 3);
+                        if (key >= N || (p.causal && key > query)) s[kb][e] = -INFINITY;
+                    }
             }
         }
+
 
         tile_barrier();  // V_j landed; every wave finished reading K_j
         set_priority<0>();  // first half of the VALU phase
         const int j_next = next_tile(j + 1);
         if (j_next < tiles) issue_k(j_next, needs16(cur_int8, cur_skip), cur_int8 != 0);
 
-        // ---- online softmax, then O^T += V^T P^T and l += 1^T P^T
+        // ---- online softmax, then O^T += V^T P^T
         if (active) {
-            half8 ph[2][2], pl[2][2];
-            softmax_tile<kFB, kPrecise>(st, s, c, ph, pl);
+            half8 ph[4], pl[4];
+            softmax_tile<kOB, kPrecise>(st, s, c, ph, pl);
             {
-                // V^T fragments two 16-feature blocks at a time, the next pair
-                // read while this pair's MFMAs issue.
-                auto v_frag = [&](int ks, int fb) {
-                    const unsigned char* v_lo = lds_v + 32 * L::kVStride * ks + v_lane[fb];
-                    return concat(read_tr16(v_lo), read_tr16(v_lo + 16 * L::kVStride));
+                // V^T fragment of step t = (key step t / kOB, feature block
+                // t % kOB), read kAhead steps before its MFMA.
+                auto v_frag = [&](int t) {
+                    const unsigned char* v_lo = lds_v + 16 * L::kVStride * (t / kOB) + v_lane[t % kOB];
+                    return concat(read_tr16(v_lo), read_tr16(v_lo + 8 * L::kVStride));
                 };
-                constexpr int kPairs = kFB;  // (ks, fb pair) stages: 2 * kFB / 2
+                constexpr int kSteps = 4 * kOB;
+                constexpr int kAhead = 3;
                 set_priority<0>();  // first half of the MFMA phase
-                half8 vf[2][2];
-                vf[0][0] = v_frag(0, 0);
-                vf[0][1] = v_frag(0, kFB > 1 ? 1 : 0);
+                half8 vf[kAhead + 1];
 #pragma unroll
-                for (int stage = 0; stage < kPairs; ++stage) {
-                    const int ks = (2 * stage) / kFB, fb0 = (2 * stage) % kFB;
-                    if (stage + 1 < kPairs) {
-                        const int ks_n = (2 * stage + 2) / kFB, fb_n = (2 * stage + 2) % kFB;
-                        vf[(stage + 1) & 1][0] = v_frag(ks_n, fb_n);
-                        vf[(stage + 1) & 1][1] = v_frag(ks_n, fb_n + 1 < kFB ? fb_n + 1 : fb_n);
-                    }
+                for (int t = 0; t < kAhead; ++t)
+                    if (t < kSteps) vf[t] = v_frag(t);
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        if (fb0 + h >= kFB) continue;
-#pragma unroll
-                        for (int b = 0; b < 2; ++b) {
-                            st.o[b][fb0 + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[stage & 1][h], ph[b][ks], st.o[b][fb0 + h], 0, 0, 0);
-                            if constexpr (kPrecise)
-                                st.o[b][fb0 + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[stage & 1][h], pl[b][ks], st.o[b][fb0 + h], 0, 0, 0);
-                        }
-                    }
-                    if (fb0 == 0) {
-                        // Row sums of exactly the fp16 P the P.V MFMAs use.
-#pragma unroll
-                        for (int b = 0; b < 2; ++b) {
-                            st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph[b][ks], st.l[b], 0, 0, 0);
-                            if constexpr (kPrecise)
-                                st.l[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pl[b][ks], st.l[b], 0, 0, 0);
-                        }
-                    }
+                for (int t = 0; t < kSteps; ++t) {
+                    if (t + kAhead < kSteps) vf[(t + kAhead) % (kAhead + 1)] = v_frag(t + kAhead);
+                    const int ks = t / kOB, fb = t % kOB;
+                    st.o[fb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[t % (kAhead + 1)], ph[ks], st.o[fb], 0, 0, 0);
+                    if constexpr (kPrecise)
+                        st.o[fb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[t % (kAhead + 1)], pl[ks], st.o[fb], 0, 0, 0);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -871,17 +833,24 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     }
 
     // ---------------------------------------------------------- epilogue
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const float l = st.l[b][0];
+    {
+        float a = st.lsum, b = st.lsum;
+        permlane32_swap(a, b);  // the row's other half, held by lane ^ 32
+        const float l = a + b;
         const float inverse = l > 0.0f ? 1.0f / l : 0.0f;
-        const int row = qw + 16 * b + i;
-        if (row >= M) continue;
-        const std::int64_t row_offset = static_cast<std::int64_t>(row) * p.o_row;
+        const int row = qw + q;
+        if (row < M) {
+            const std::int64_t row_offset = static_cast<std::int64_t>(row) * p.o_row;
 #pragma unroll
-        for (int fb = 0; fb < kFB; ++fb) {
-            const int feature = 16 * fb + 4 * g;
-            store_output(Oh, p.o_dtype, row_offset + feature, st.o[b][fb] * inverse, d - feature, kVector);
+            for (int fb = 0; fb < kOB; ++fb)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    // Output row R = 8 r4 + 4 h (+ 0..3) of block fb is feature
+                    // 16 fb + R (R < 16) or kDP / 2 + 16 fb + R - 16.
+                    const int feature = (r4 < 2 ? 0 : kDP / 2 - 16) + 16 * fb + 8 * r4 + 4 * h;
+                    const float4v value{st.o[fb][4 * r4], st.o[fb][4 * r4 + 1], st.o[fb][4 * r4 + 2], st.o[fb][4 * r4 + 3]};
+                    store_output(Oh, p.o_dtype, row_offset + feature, value * inverse, d - feature, kVector);
+                }
         }
     }
 }

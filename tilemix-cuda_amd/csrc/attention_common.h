@@ -84,36 +84,13 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
 }
 
 // Cross-lane exchange without LDS: with a == b == x on entry,
-// v_permlane16_swap leaves a = x of rows {0, 0, 2, 2} and b = x of rows
-// {1, 1, 3, 3} (rows of 16 lanes); v_permlane32_swap leaves a = x of the lower
-// half in both halves and b = x of the upper half. So max(a, b) is
-// the butterfly step with partner lane ^ 16 / ^ 32. Inline assembly because
-// the compiler builtins for these swaps get folded as if both results were
-// the same value; s_nop 1 covers the VALU-write -> permlane-read hazard.
-__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
+// v_permlane32_swap leaves a = x of the lower half in both halves and b = x
+// of the upper half, so max(a, b) or a + b combines lanes l and l ^ 32.
+// Inline assembly because the compiler builtin for this swap gets folded as
+// if both results were the same value; s_nop 1 covers the VALU-write ->
+// permlane-read hazard.
 __device__ __forceinline__ void permlane32_swap(float& a, float& b) {
     asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-// Maximum over lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row).
-__device__ __forceinline__ float row_max4(float x) {
-    float a = x, b = x;
-    permlane16_swap(a, b);
-    float c = max3(a, b, b), e = c;
-    permlane32_swap(c, e);
-    return max3(c, e, e);
-}
-// row_max4 of two independent values, their cross-lane steps interleaved.
-__device__ __forceinline__ void row_max4_pair(float& x, float& y) {
-    float a = x, b = x, c = y, d = y;
-    permlane16_swap(a, b);
-    permlane16_swap(c, d);
-    float e = max3(a, b, b), f = e, h = max3(c, d, d), k = h;
-    permlane32_swap(e, f);
-    permlane32_swap(h, k);
-    x = max3(e, f, f);
-    y = max3(h, k, k);
 }
 
 
