@@ -101,14 +101,17 @@ struct Layout {
     static_assert(kKBytes % 1024 == 0 && kVBytes % 1024 == 0 && kK8Bytes % 1024 == 0,
                   "tiles are whole wave loads");
     // Chunk rotation of a rotated row of kChunks 16-byte chunks. Key rows
-    // (K, K8) are read as 32 consecutive rows x one chunk per half-wave:
-    // rotations that put every pair of such rows on its own bank group. Value
-    // rows are read by ds_read_b64_tr_b16 in 4-row x 16-feature blocks.
+    // (K, K8) are read as 32 consecutive rows x one chunk per half-wave: the
+    // rows that share one 256-byte sweep of the banks share a rotation, and
+    // consecutive sweeps step it by one chunk (measured on 64-byte K8 rows:
+    // 13 % of LDS-active cycles in bank conflicts with a rotation that steps
+    // every two rows, 0.9 % with this one). Value rows are read by
+    // ds_read_b64_tr_b16 in 4-row x 16-feature blocks.
     template <int kChunks, bool kKey>
     __device__ static int rot(int row) {
         static_assert(kChunks == 16 || kChunks == 8 || kChunks == 4, "rotated rows are 256, 128 or 64 bytes");
         if constexpr (kKey)
-            return kChunks == 16 ? row & 15 : kChunks == 8 ? (row >> 1) & 7 : ((row >> 1) ^ (row >> 3)) & 3;
+            return kChunks == 16 ? row & 15 : kChunks == 8 ? (row >> 1) & 7 : (row >> 2) & 3;
         else
             return kChunks == 16 ? (2 * row) & 15 : kChunks == 8 ? row & 6 : 2 * ((row >> 2) & 1);
     }
