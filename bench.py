@@ -329,8 +329,9 @@ def measured_traffic(workload: str):
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
         return None
-    entry = json.loads(path.read_text()).get("attention_kernel")
-    if not entry or entry.get("workload") != workload:
+    entries = json.loads(path.read_text()).get("attention_kernel") or []
+    entry = next((e for e in entries if e.get("workload") == workload), None)
+    if entry is None:
         return None
     current = source_stamp()
     if entry.get("source_stamp") != current:
