@@ -22,7 +22,11 @@ pytestmark = pytest.mark.gpu
 
 INT_MAX = 2**31 - 1
 
-DENSE_CASES = [(3, 33, d, "random", False) for d in (1, 15, 16, 17, 31, 32, 33, 49, 63, 64, 65, 81, 97, 113, 127, 128)] + [
+# The head-dimension sweep covers each kernel layout class: padded and rotated
+# K / V rows, 64- and 128-byte K8 rows, and (d % 16 == 0, aligned runs) the
+# vector path of every padded head dimension 32 * ceil(d / 32).
+DENSE_CASES = [(3, 33, d, "random", False)
+               for d in (1, 15, 16, 17, 31, 32, 33, 48, 49, 63, 64, 65, 80, 81, 96, 97, 112, 113, 127, 128)] + [
     (1, 1, 1, "random", False), (3, 5, 7, "random", False), (15, 31, 15, "random", False),
     (16, 32, 16, "random", False), (17, 33, 17, "random", False), (31, 63, 31, "random", False),
     (32, 64, 32, "random", False), (33, 65, 33, "random", False), (35, 67, 65, "random", False),
@@ -158,7 +162,7 @@ ROUTING_SHAPES = [((35, 67, 17, "random", False), 2), ((17, 2048, 5, "random", F
 ROUTING_CASES = [(shape, group, pattern, True) for shape, group in ROUTING_SHAPES
                  for pattern in ("fp16", "int8-requested", "mixed")]
 ROUTING_CASES += [((3, 33, d, "random", False), 1, pattern, True)
-                  for d in (1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128)
+                  for d in (1, 15, 16, 17, 31, 32, 33, 48, 63, 64, 65, 80, 96, 112, 127, 128)
                   for pattern in ("fp16", "int8-requested", "mixed")]
 ROUTING_CASES += [((17, 2051, 5, "random", False), 1, "implicit-fp16", True),
                   ((35, 67, 17, "random", False), 2, "mixed", False)]
