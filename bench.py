@@ -25,8 +25,14 @@ headline attention launch goes from about 0.39 ms to 0.31 ms after roughly
 rate. The JSON line reports W as requested and the steps actually run; the
 timed region is exactly K steps either way.
 
+The warm-up ends with a shader-clock sample: rocm-smi reads the clock while
+more untimed steps run (``roofline.sclk_mhz_sampled``). The MFMA peaks are
+quoted at 2.4 GHz; with N(0,1) operands the card holds a lower clock under its
+power limit (``--input-scale 0`` shows the same kernel at 2.4 GHz).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--min-warmup-ms T] [--config 3]
-                       [--precise] [--no-check] [--no-cpu-baseline]
+                       [--precise] [--no-check] [--no-cpu-baseline] [--no-clock]
+                       [--input-scale F]
 """
 from __future__ import annotations
 
@@ -65,6 +71,12 @@ def parse_args():
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="after timing, run one device copy of this many MiB on the bench stream "
                         "(calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE against known bytes)")
+    p.add_argument("--no-clock", action="store_true",
+                   help="skip the rocm-smi shader-clock sample taken after the timed steps")
+    p.add_argument("--input-scale", type=float, default=1.0,
+                   help="diagnostic: multiply Q, K and V by this factor after the routing codes are "
+                        "drawn from the unscaled inputs (same routes, same INT8 codes, smaller "
+                        "operands); used to show how the sustained clock depends on the data")
     p.add_argument("--per-head", choices=["demo", "config"], default=None,
                    help="time the drop-in per-head API (launch_fused_fp16_attention, precise P.V) instead: "
                         "'demo' = the reference demo workload (M=1000 N=1003 d=128, g=2, mask 0xaaaa...), "
@@ -100,6 +112,9 @@ def main() -> int:
     log(w.describe())
     Q, K, V = workloads.make_inputs(w, args.seed)
     codes = workloads.make_codes(w, args.seed, Q, K)
+    if args.input_scale != 1.0:
+        Q, K, V = ((x.float() * args.input_scale).to(torch.float16) for x in (Q, K, V))
+        log(f"inputs scaled by {args.input_scale:g} (routing codes from the unscaled inputs)")
     route_np, skip_np = workloads.pack_heads(codes, w.key_tiles_per_group)
     work = workloads.work(w, codes)
     heads, S, D = w.heads, w.S, w.D
@@ -135,6 +150,12 @@ def main() -> int:
                 step()
             warmup_run += 8
             torch.cuda.synchronize()
+        # The shader clock under sustained load, sampled while more untimed steps run.
+        sclk = None
+        if not args.no_clock:
+            sclk, sample_steps = sample_sclk_mhz(step, torch.cuda.synchronize)
+            warmup_run += sample_steps
+            log(f"sampled shader clock: {sclk} MHz")
         warmup_ms = (time.perf_counter() - warm_start) * 1e3
         log(f"warm-up: {warmup_run} steps in {warmup_ms:.1f} ms ({args.warmup} requested, "
             f"minimum {args.min_warmup_ms:g} ms)")
@@ -199,8 +220,12 @@ def main() -> int:
             "kernel_ms": round(attn_ms, 5),
             "achieved_hbm_gbs": None,
             "peak_basis": "blended: ops_int8/5033.2T + flops_fp16/2516.6T",
+            "sclk_mhz_sampled": sclk,
+            "sclk_mhz_peak_basis": 2400,
         },
     }
+    if args.input_scale != 1.0:
+        result["data"] += f"; Q, K, V scaled by {args.input_scale:g} after routing (diagnostic run)"
 
     measured = measured_traffic(w.describe())
     if measured is not None and "stale" in measured:
@@ -320,6 +345,41 @@ def source_stamp() -> str:
     for name in STAMPED_SOURCES:
         h.update(name.encode() + b"\0" + (ROOT / name).read_bytes() + b"\0")
     return h.hexdigest()[:16]
+
+
+def sample_sclk_mhz(step, sync) -> tuple[float | None, int]:
+    """Shader clock (MHz) that rocm-smi reports while bench steps keep the GPU busy (None when
+    rocm-smi is unavailable), and the number of steps run meanwhile. The MI355X holds its 2.4 GHz maximum only while it is under
+    its power limit; with N(0,1) operands this kernel runs below it (zero operands: at it)."""
+    import subprocess
+    import threading
+
+    reading: dict = {}
+
+    def read():
+        time.sleep(0.2)
+        try:
+            r = subprocess.run(["rocm-smi", "--showclocks", "--csv"], capture_output=True, text=True,
+                               timeout=20)
+            lines = [line for line in r.stdout.splitlines() if line.strip()]
+            header = next(line for line in lines if line.startswith("device"))
+            row = next(line for line in lines if line.startswith("card"))
+            field = row.split(",")[header.split(",").index("sclk clock speed:")]
+            reading["mhz"] = float("".join(ch for ch in field if ch.isdigit() or ch == "."))
+        except Exception:  # no rocm-smi, no permission, other output layout
+            pass
+
+    reader = threading.Thread(target=read, daemon=True)
+    reader.start()
+    start = time.perf_counter()
+    steps = 0
+    while reader.is_alive() and time.perf_counter() - start < 25.0:
+        for _ in range(8):
+            step()
+        steps += 8
+        sync()
+    reader.join(timeout=1.0)
+    return reading.get("mhz"), steps
 
 
 def measured_traffic(workload: str):
