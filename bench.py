@@ -92,9 +92,9 @@ def log(msg: str) -> None:
 def main() -> int:
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build runs on one GPU only: the TileMix path shards across "
-                          "GPUs by head with no exchange (see DESIGN.md), but multi-GPU runs are not "
-                          "part of this build; run with --gpus 1"}))
+        print(json.dumps({"error": "this build runs on one GPU only: the TileMix path would shard "
+                          "across GPUs by head with no exchange between them, but multi-GPU runs are "
+                          "not part of this build; run with --gpus 1"}))
         return 2
 
     import torch
@@ -347,6 +347,26 @@ def source_stamp() -> str:
     return h.hexdigest()[:16]
 
 
+def parse_sclk_csv(text: str) -> float | None:
+    """The shader clock in MHz from `rocm-smi --showclocks --csv` output (header row starting
+    'device' with a 'sclk clock speed:' column, then one row per card, e.g. '(2040Mhz)'), or
+    None when the layout is not that one."""
+    lines = [line.strip() for line in text.splitlines() if line.strip()]
+    header = next((line for line in lines if line.startswith("device")), None)
+    row = next((line for line in lines if line.startswith("card")), None)
+    if header is None or row is None:
+        return None
+    columns = header.split(",")
+    if "sclk clock speed:" not in columns:
+        return None
+    fields = row.split(",")
+    index = columns.index("sclk clock speed:")
+    if index >= len(fields):
+        return None
+    digits = "".join(ch for ch in fields[index] if ch.isdigit() or ch == ".")
+    return float(digits) if digits else None
+
+
 def sample_sclk_mhz(step, sync) -> tuple[float | None, int]:
     """Shader clock (MHz) that rocm-smi reports while bench steps keep the GPU busy (None when
     rocm-smi is unavailable), and the number of steps run meanwhile. The MI355X holds its 2.4 GHz maximum only while it is under
@@ -361,12 +381,8 @@ def sample_sclk_mhz(step, sync) -> tuple[float | None, int]:
         try:
             r = subprocess.run(["rocm-smi", "--showclocks", "--csv"], capture_output=True, text=True,
                                timeout=20)
-            lines = [line for line in r.stdout.splitlines() if line.strip()]
-            header = next(line for line in lines if line.startswith("device"))
-            row = next(line for line in lines if line.startswith("card"))
-            field = row.split(",")[header.split(",").index("sclk clock speed:")]
-            reading["mhz"] = float("".join(ch for ch in field if ch.isdigit() or ch == "."))
-        except Exception:  # no rocm-smi, no permission, other output layout
+            reading["mhz"] = parse_sclk_csv(r.stdout)
+        except Exception:  # no rocm-smi, no permission
             pass
 
     reader = threading.Thread(target=read, daemon=True)

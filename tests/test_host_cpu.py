@@ -193,3 +193,23 @@ def test_bench_refuses_more_than_one_gpu():
     assert proc.returncode == 2, proc.stderr
     line = json.loads(proc.stdout.strip().splitlines()[-1])
     assert "one GPU" in line["error"]
+
+
+def test_bench_reads_the_shader_clock_from_rocm_smi_csv():
+    """bench.py's clock sample parses `rocm-smi --showclocks --csv` as printed on the
+    MI355X box (header row, then one row per card), and returns None for any other
+    layout rather than a wrong number."""
+    import importlib.util
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    spec = importlib.util.spec_from_file_location("bench_module", root / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    seen = ("device,mclk clock speed:,mclk clock level:,sclk clock speed:,sclk clock level:\n"
+            "card0,(2000Mhz),0,(2040Mhz),1\n")
+    assert bench.parse_sclk_csv(seen) == 2040.0
+    assert bench.parse_sclk_csv("\n" + seen + "\n") == 2040.0
+    assert bench.parse_sclk_csv("device,mclk clock speed:\ncard0,(2000Mhz)\n") is None
+    assert bench.parse_sclk_csv("device,sclk clock speed:\ncard0,()\n") is None
+    assert bench.parse_sclk_csv("") is None
