@@ -8,23 +8,25 @@ precise P.V that this API always takes), checked like the reference's own routin
 (src/tests/tilemix_test.cu:487-500): quantized operands and every INT32 dot
 of an INT8 cell bit for bit, the routing trace exactly, and O against the
 fp64 TileMix oracle at 1e-5 + 1e-4 |x|. d = 128 runs with O 16-byte aligned
-(vector path) and 4-byte aligned (scalar path); d = 64 with the vector path.
+(vector path) and 4-byte aligned (scalar path); d = 64 with the vector path;
+M = 4000, N = 4001 puts a partial tile at the end of both (vector path). K and
+V are followed by 64 NaN rows in every case, so a read past key N - 1 shows.
 """
 import numpy as np
 import pytest
 
 from helpers import GUARD_DOT, GUARD_F32, GUARD_TRACE, compare, dev, dev_half, guarded, guarded_lead, host, \
-    reference_group_words
+    nan_padded_rows, reference_group_words
 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("d,lead", [(128, 4), (128, 1), (64, 4)],
-                         ids=["d128-vector", "d128-scalar", "d64-vector"])
-def test_per_head_api_headline_size(tm, oracle_lib, cuda, d, lead):
+@pytest.mark.parametrize("m,n,d,lead", [(4096, 4096, 128, 4), (4096, 4096, 128, 1), (4096, 4096, 64, 4),
+                                        (4000, 4001, 128, 4)],
+                         ids=["d128-vector", "d128-scalar", "d64-vector", "ragged-d128-vector"])
+def test_per_head_api_headline_size(tm, oracle_lib, cuda, m, n, d, lead):
     import torch
 
-    m = n = 4096
     group = 2
     query_tiles, key_tiles = (m + 15) // 16, (n + 31) // 32
     words, expected_bits = reference_group_words(query_tiles, key_tiles, group, "mixed")
@@ -32,7 +34,9 @@ def test_per_head_api_headline_size(tm, oracle_lib, cuda, d, lead):
     q, k, v = oracle_lib.make_inputs(m, n, d, "random")
     q8_ref, qs_ref = oracle_lib.quantize(q, 128)
     k8_ref, ks_ref = oracle_lib.quantize(k, 64)
-    dq, dk, dv = dev_half(q), dev_half(k), dev_half(v)
+    # K / V followed by 64 NaN rows: a read past key n - 1 would turn into a NaN output.
+    dq = dev_half(q)
+    dk, dv = dev_half(nan_padded_rows(k.reshape(n, d))), dev_half(nan_padded_rows(v.reshape(n, d)))
     # lead 4: O 16-byte aligned after the guard words (vector path); lead 1: O only 4-byte aligned (scalar path).
     out = guarded_lead(m * d, np.float32, GUARD_F32, fill=np.nan, lead=lead)
     mask = dev(words)
