@@ -6,7 +6,9 @@
   on the vector (d % 16 == 0) and element-wise (odd d) paths;
 * tilemix_quantize_qk_strided equals the contiguous batched quantizer;
 * a head whose K / V span more than 2 GiB (4 MiB row stride) takes the
-  element-wise path and gives the contiguous run's bits.
+  element-wise path and gives the contiguous run's bits;
+* a seeded sweep of 12 more shapes (ragged S, d from 8 to 128, causal,
+  precise, routed, fp16 or bf16 O) holds both of the first two properties.
 """
 from __future__ import annotations
 
@@ -156,3 +158,40 @@ def test_heads_past_2gib_take_the_elementwise_path(tm, cuda):
             assert torch.equal(x.view(torch.int32), y.view(torch.int32)), name
         else:
             assert torch.equal(x, y), name
+
+
+def _layout_cases():
+    rng = np.random.default_rng(20261203)
+    dims = [8, 17, 32, 48, 64, 96, 100, 128]
+    cases = []
+    for i in range(12):  # every head dimension at least once, the other options drawn
+        cases.append((int(rng.integers(1, 5)), int(rng.integers(1, 700)), dims[i % len(dims)],
+                      bool(rng.random() < 0.5), bool(rng.random() < 0.5), bool(rng.random() < 0.7),
+                      int(rng.integers(1, 3))))
+    return cases
+
+
+LAYOUT_CASES = _layout_cases()
+
+
+@pytest.mark.parametrize("heads,S,d,causal,precise,routed,dtype", LAYOUT_CASES,
+                         ids=[f"h{c[0]}-S{c[1]}-d{c[2]}{'-causal' if c[3] else ''}{'-precise' if c[4] else ''}"
+                              f"{'-routed' if c[5] else ''}-{'f16' if c[6] == 1 else 'bf16'}" for c in LAYOUT_CASES])
+def test_layout_and_output_type_sweep(tm, cuda, heads, S, d, causal, precise, routed, dtype):
+    """Seeded shapes: the row-strided [S, H, D] run equals the contiguous [H, S, D] run bit for bit
+    (O, Q8/K8 and scales), and its fp16 / bf16 O equals the contiguous fp32 O rounded."""
+    import torch
+
+    print(f"layout sweep heads={heads} S={S} d={d} causal={causal} precise={precise} routed={routed} "
+          f"dtype={dtype}", flush=True)
+    Q, K, V = _inputs(torch, heads, S, d, 7 * S + d)
+    route = _routes(torch, heads, S, 2, S) if routed else None
+    ref = _run(tm, torch, Q, K, V, heads, S, d, tm.DTYPE_F32, "hsd", causal, precise, route)
+    strided = _run(tm, torch, Q, K, V, heads, S, d, tm.DTYPE_F32, "shd", causal, precise, route)
+    typed = _run(tm, torch, Q, K, V, heads, S, d, dtype, "shd", causal, precise, route)[0]
+    assert torch.isfinite(ref[0]).all()
+    for a, b in zip(ref, strided):
+        assert torch.equal(a.view(torch.int8) if a.dtype != torch.int8 else a,
+                           b.view(torch.int8) if b.dtype != torch.int8 else b), "strided run differs"
+    rounded = ref[0].half() if dtype == tm.DTYPE_F16 else ref[0].bfloat16()
+    assert torch.equal(typed.view(torch.int16), rounded.view(torch.int16)), "typed output is not the rounded fp32 O"
