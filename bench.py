@@ -222,6 +222,10 @@ def main() -> int:
             "peak_basis": "blended: ops_int8/5033.2T + flops_fp16/2516.6T",
             "sclk_mhz_sampled": sclk,
             "sclk_mhz_peak_basis": 2400,
+            # frac against the peaks scaled to the sampled clock: how close the kernel runs to
+            # what the card delivers at the clock it holds under this load (frac itself stays
+            # against the 2.4 GHz peaks)
+            "frac_at_sampled_sclk": round(achieved / blended_peak * 2400.0 / sclk, 4) if sclk else None,
         },
     }
     if args.input_scale != 1.0:
