@@ -77,6 +77,9 @@ def parse_args():
                    help="diagnostic: multiply Q, K and V by this factor after the routing codes are "
                         "drawn from the unscaled inputs (same routes, same INT8 codes, smaller "
                         "operands); used to show how the sustained clock depends on the data")
+    p.add_argument("--routing", action="store_true",
+                   help="time the device routing producer for --config's router instead (tile codes, "
+                        "then route / skip words), with HBM rates against the algorithmic bytes")
     p.add_argument("--per-head", choices=["demo", "config"], default=None,
                    help="time the drop-in per-head API (launch_fused_fp16_attention, precise P.V) instead: "
                         "'demo' = the reference demo workload (M=1000 N=1003 d=128, g=2, mask 0xaaaa...), "
@@ -107,6 +110,9 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.per_head:
         print(json.dumps(per_head_bench(args)), flush=True)
+        return 0
+    if args.routing:
+        print(json.dumps(routing_bench(args)), flush=True)
         return 0
     w = workloads.WORKLOADS[args.config]
     log(w.describe())
@@ -249,6 +255,90 @@ def main() -> int:
 
     print(json.dumps(result), flush=True)
     return 0
+
+
+def routing_bench(args) -> dict:
+    """The device routing producer on --config's shape: stage 1 writes one code per tile
+    (tilemix_tiles_bernoulli / _causal_band / _three_way, or the importance router, which
+    reads all of Q and K for its tile maxima), stage 2 packs the codes into TileMixRouting
+    words (tilemix_routes_from_tiles). Each stage is timed with HIP events over --steps
+    calls after the clock warm-up; bytes are the algorithmic ones (inputs read once, codes
+    and words written once). For the importance router the device codes are compared with
+    the host router over the same data."""
+    import torch
+    import tilemix
+    from tilemix import routing, workloads
+
+    w = workloads.WORKLOADS[args.config]
+    heads, S, D, g = w.heads, w.S, w.D, w.key_tiles_per_group
+    tr, tk = (128, 64) if w.router in ("causal_band", "importance") else (64, 64)
+    tq, tkk = (S + tr - 1) // tr, (S + tk - 1) // tk
+    dev = "cuda:0"
+    codes = torch.empty((heads, tq, tkk), dtype=torch.uint8, device=dev)
+    words = tilemix.routing_word_count(S, S, g)
+    route = torch.empty(heads * words, dtype=torch.int64, device=dev)
+    skip = torch.empty_like(route)
+    stream = torch.cuda.Stream()
+    seed = args.seed
+    if w.router == "importance":
+        Q, K, _ = workloads.make_inputs(w, args.seed)
+        need = tilemix.importance_workspace_bytes(heads, S, S, tr, tk)
+        workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=dev)
+        stage1_bytes = 2 * heads * S * D * 2 + codes.numel()
+
+        def stage1():
+            tilemix.check(tilemix.tiles_importance(Q, K, heads, S, S, D, tr, tk, 0.25, workspace, need, codes,
+                                                   stream=stream), "importance")
+    else:
+        stage1_bytes = codes.numel()
+
+        def stage1():
+            if w.router == "bernoulli":
+                rc = tilemix.tiles_bernoulli(codes, heads, S, S, tr, tk, 0.5, seed, stream=stream)
+            elif w.router == "causal_band":
+                rc = tilemix.tiles_causal_band(codes, heads, S, tr, tk, 8, 0.5, seed, stream=stream)
+            else:
+                rc = tilemix.tiles_three_way(codes, heads, S, S, tr, tk, 0.3, 0.4, seed, stream=stream)
+            tilemix.check(rc, w.router)
+
+    def stage2():
+        tilemix.check(tilemix.routes_from_tiles(codes, heads, S, S, tr, tk, g, route, skip, stream=stream), "pack")
+
+    stage2_bytes = codes.numel() + 2 * route.numel() * 8
+
+    def timed(fn):
+        with torch.cuda.stream(stream):
+            start = time.perf_counter()
+            while (time.perf_counter() - start) * 1e3 < args.min_warmup_ms:
+                for _ in range(8):
+                    fn()
+                torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    stages = []
+    for name, fn, nbytes in ((f"tile codes ({w.router})", stage1, stage1_bytes),
+                             ("routes_from_tiles", stage2, stage2_bytes)):
+        ms = timed(fn)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        stages.append({"stage": name, "ms": round(ms, 5), "bytes": int(nbytes), "gbs": round(gbs, 1),
+                       "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)})
+    result = {"metric": "device routing producer, per call", "config": {"workload": w.describe(),
+              "tile": [tr, tk], "key_tiles_per_group": g, "tiles_per_head": tq * tkk}, "steps": args.steps,
+              "stages": stages}
+    if w.router == "importance":
+        got = codes.cpu().numpy()
+        q_amax = Q.view(heads, tq, tr * D).abs().amax(-1).float().cpu().numpy()
+        k_amax = K.view(heads, tkk, tk * D).abs().amax(-1).float().cpu().numpy()
+        match = all(np.array_equal(got[h], routing.importance_top_fraction(
+            q_amax[h], k_amax[h], S, S, D, tr, tk, 0.25)[:: tr // 16, :: tk // 32][:tq, :tkk]) for h in range(heads))
+        result["codes_equal_host_router"] = bool(match)
+    return result
 
 
 def per_head_bench(args) -> dict:

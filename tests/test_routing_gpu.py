@@ -59,8 +59,12 @@ def test_builders_match_host_restatement(tm, cuda, heads, M, N, tr, tk, seed):
 def _host_importance(q, k, M, N, d, tr, tk, fraction):
     """Per-tile maxima from the same fp16 data, then the host router (tile codes)."""
     tq, tkk = ref.tile_grid(M, N, tr, tk)
-    qa = np.array([np.abs(q[i * tr:(i + 1) * tr].astype(np.float32)).max() for i in range(tq)])
-    ka = np.array([np.abs(k[j * tk:(j + 1) * tk].astype(np.float32)).max() for j in range(tkk)])
+    def amax(block):  # NaN elements passed over, as fmaxf from 0 does
+        a = np.abs(block.astype(np.float32))
+        return np.where(np.isnan(a), np.float32(0), a).max()
+
+    qa = np.array([amax(q[i * tr:(i + 1) * tr]) for i in range(tq)])
+    ka = np.array([amax(k[j * tk:(j + 1) * tk]) for j in range(tkk)])
     cells = routing.importance_top_fraction(qa, ka, M, N, d, tr, tk, fraction)
     return cells[:: tr // 16, :: tk // 32][:tq, :tkk]
 
@@ -72,6 +76,15 @@ def _host_importance(q, k, M, N, d, tr, tk, fraction):
     (1, 512, 512, 32, 128, 64, 0.0, "normal"),
     (1, 512, 512, 32, 128, 64, 1.0, "normal"),
     (4, 16384, 16384, 128, 128, 64, 0.25, "outlier"),
+    (2, 700, 900, 36, 64, 64, 0.4, "normal"),  # d % 8 != 0: the element-wise maximum
+    (2, 1000, 1200, 64, 64, 64, 0.3, "nan"),
+    (2, 4096, 4096, 64, 64, 64, 0.37, "ties"),  # ties ranked across several 1024-tile chunks
+    (1, 3000, 50, 32, 16, 64, 0.5, "normal"),  # one key tile per row
+    (1, 130, 70000, 64, 64, 64, 0.3, "ties"),  # rows longer than the select's 1024 threads
+    (1, 2048, 4096, 16, 16, 32, 0.4, "ties"),  # 16384 tiles: keys held in registers, ties ranked
+    (2, 1000, 5000, 16, 16, 32, 0.3, "normal"),  # 9891 tiles: a ragged last wave of register keys
+    (1, 1000, 5000, 16, 16, 32, 0.75, "zeros"),  # selected key 0, tied with the ragged padding
+    (1, 4096, 8192, 16, 16, 32, 0.45, "ties"),  # 65536 tiles: keys recomputed each pass
 ])
 def test_importance_matches_host_router(tm, cuda, heads, M, N, d, tr, tk, fraction, pattern):
     import torch
@@ -85,12 +98,20 @@ def test_importance_matches_host_router(tm, cuda, heads, M, N, d, tr, tk, fracti
         ch = torch.tensor([3, 17, 40][: max(1, d // 48)], device="cuda")
         q[..., ch] *= 8.0
         k[..., ch] *= 8.0
+    if pattern == "zeros":  # half the query tiles all zero: many keys equal to 0
+        q[:, : M // 2] = 0.0
     if pattern == "ties":  # many equal tile maxima: ranks decided by tile index
         q = torch.round(q * 2) / 2
         k = torch.round(k * 2) / 2
         q.clamp_(-2, 2)
         k.clamp_(-2, 2)
     q, k = q.half().contiguous(), k.half().contiguous()
+    if pattern == "nan":  # scattered NaNs, and one Q tile and one K tile that are all NaN
+        q[:, 5, 3] = float("nan")
+        q[:, 300, :] = float("nan")
+        q[:, tr:2 * tr, :] = float("nan")
+        k[:, 7, 0] = float("nan")
+        k[:, (N - 1) // tk * tk:, :] = float("nan")
     tq, tkk = ref.tile_grid(M, N, tr, tk)
     need = tm.importance_workspace_bytes(heads, M, N, tr, tk)
     ws = torch.empty(need // 4, dtype=torch.float32, device="cuda")

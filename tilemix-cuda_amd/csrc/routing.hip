@@ -100,12 +100,18 @@ __global__ void three_way_kernel(std::uint8_t* codes, int rows, int tiles_k, flo
 
 // Absolute maximum of each tile row block of Q (blockIdx.x < tiles_q) and
 // each key block of K (the rest), per head (blockIdx.y): amax[head][tiles_q +
-// tiles_k].
+// tiles_k]. NaN elements are passed over, as fmaxf does. kVector (d % 8 == 0,
+// 16-byte aligned heads): 16-byte loads and the maximum over fp16 bit
+// patterns with the sign cleared (unsigned order is value order for them;
+// NaN patterns sort above +inf, so a maximum above 0x7c00 sends the block
+// through a second pass that leaves NaNs out).
+template <bool kVector>
 __global__ __launch_bounds__(256) void tile_absmax_kernel(const std::uint16_t* Q, const std::uint16_t* K, int M,
                                                           int N, int d, std::int64_t q_stride,
                                                           std::int64_t k_stride, int tiles_q, int tiles_k,
                                                           int tile_rows, int tile_keys, float* amax) {
     __shared__ float partial[256 / kWave];
+    __shared__ unsigned partial_bits[256 / kWave];
     const int head = blockIdx.y;
     const bool is_q = static_cast<int>(blockIdx.x) < tiles_q;
     const int block = is_q ? static_cast<int>(blockIdx.x) : static_cast<int>(blockIdx.x) - tiles_q;
@@ -115,125 +121,326 @@ __global__ __launch_bounds__(256) void tile_absmax_kernel(const std::uint16_t* Q
     const int last = min(rows, first + span);
     const std::uint16_t* x = (is_q ? Q + head * q_stride : K + head * k_stride) + static_cast<std::int64_t>(first) * d;
     const std::int64_t count = static_cast<std::int64_t>(last - first) * d;
-    float m = 0.0f;
-    for (std::int64_t e = threadIdx.x; e < count; e += 256) m = fmaxf(m, fabsf(half_bits_to_float(x[e])));
-    m = wave_max(m);
-    if ((threadIdx.x & (kWave - 1)) == 0) partial[threadIdx.x / kWave] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        m = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
-        amax[static_cast<std::int64_t>(head) * (tiles_q + tiles_k) + blockIdx.x] = m;
+    const std::int64_t slot = static_cast<std::int64_t>(head) * (tiles_q + tiles_k) + blockIdx.x;
+    if constexpr (kVector) {
+        // Eight 16-byte loads in flight per thread, then their maximum.
+        constexpr int kLoads = 8;
+        const std::int64_t chunks = count / 8;
+        unsigned top = 0;
+        for (std::int64_t base = threadIdx.x; base < chunks; base += kLoads * 256) {
+            uint4v v[kLoads];
+#pragma unroll
+            for (int u = 0; u < kLoads; ++u) {
+                const std::int64_t c = base + u * 256;
+                v[u] = c < chunks ? *reinterpret_cast<const uint4v*>(x + 8 * c) : uint4v{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < kLoads; ++u)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) top = max_u16x2(top, v[u][w] & 0x7fff7fffu);
+        }
+        unsigned bits = wave_max_bits(max(top & 0xffffu, top >> 16));
+        if ((threadIdx.x & (kWave - 1)) == 0) partial_bits[threadIdx.x / kWave] = bits;
+        __syncthreads();
+        bits = max(max(partial_bits[0], partial_bits[1]), max(partial_bits[2], partial_bits[3]));
+        if (bits > 0x7c00u) {
+            // A NaN in the block: the maximum over the other elements.
+            unsigned clean = 0;
+            for (std::int64_t e = threadIdx.x; e < count; e += 256) {
+                const unsigned h = x[e] & 0x7fffu;
+                clean = h <= 0x7c00u ? max(clean, h) : clean;
+            }
+            clean = wave_max_bits(clean);
+            __syncthreads();
+            if ((threadIdx.x & (kWave - 1)) == 0) partial_bits[threadIdx.x / kWave] = clean;
+            __syncthreads();
+            bits = max(max(partial_bits[0], partial_bits[1]), max(partial_bits[2], partial_bits[3]));
+        }
+        if (threadIdx.x == 0) amax[slot] = half_bits_to_float(static_cast<std::uint16_t>(bits));
+    } else {
+        float m = 0.0f;
+        for (std::int64_t e = threadIdx.x; e < count; e += 256) m = fmaxf(m, fabsf(half_bits_to_float(x[e])));
+        m = wave_max(m);
+        if ((threadIdx.x & (kWave - 1)) == 0) partial[threadIdx.x / kWave] = m;
+        __syncthreads();
+        if (threadIdx.x == 0) amax[slot] = fmaxf(fmaxf(partial[0], partial[1]), fmaxf(partial[2], partial[3]));
     }
 }
 
 // One workgroup per head: the `count` tiles with the largest amax_Q(i) *
 // amax_K(j) (exact in fp32: both are fp16 magnitudes; the factor d does not
 // change the order) become FP16, ties going to the lower tile index; the
-// rest INT8. Radix select on the float bits (non-negative, so integer order
-// is value order), then one pass in index order that ranks the ties.
+// rest INT8. The keys are the products' float bits (non-negative, so integer
+// order is value order) minus the head's smallest key; a radix select over
+// the bits of (largest - smallest), at most 11 bits a pass (three passes
+// cover any range), finds the count-th largest key with one histogram of
+// 2048 bins and a block-wide scan over its bins per pass. Then one pass in
+// index order sets the codes, ranking the ties with wave ballots only when
+// some of the keys equal to the selected one stay INT8.
+//
+// kKeys > 0 (a head of at most 1024 kKeys tiles): wave w holds tiles
+// [64 kKeys w, 64 kKeys (w + 1)) in registers, tile 64 kKeys w + 64 u + lane
+// in keys[u], so a pass reads no memory, the code stores of a wave are
+// contiguous, and the ties before a tile are those of earlier waves plus the
+// wave's own earlier slots and lanes. Tiles past the end take the smallest
+// key, which leaves the selection unchanged (count < total, and their indices
+// sort them after every valid tile of equal key); they are never stored.
+// kKeys == 0: thread t recomputes tiles t, t + 1024, ... each pass, its (row,
+// column) advancing by a fixed step, and ties are ranked 1024 tiles at a time.
+template <int kKeys>
 __global__ __launch_bounds__(kSelectThreads) void importance_select_kernel(const float* amax, int tiles_q,
                                                                             int tiles_k, std::int64_t count,
                                                                             std::uint8_t* codes) {
+    constexpr int kWaves = kSelectThreads / kWave;
+    constexpr int kDigitBits = 11;
+    constexpr int kBins = 1 << kDigitBits;
+    static_assert(kBins == 2 * kSelectThreads, "two bins per thread in the digit scan");
     extern __shared__ float factors[];  // tiles_q + tiles_k
-    __shared__ unsigned histogram[256];
-    __shared__ unsigned scan[kSelectThreads];
-    __shared__ unsigned chosen_digit;
-    __shared__ unsigned long long still_needed;
+    __shared__ unsigned histogram[kBins];
+    __shared__ unsigned wave_low[kWaves], wave_high[kWaves];
+    __shared__ unsigned chosen_digit, still_needed, equal_keys;
     const int head = blockIdx.x;
     const int t = threadIdx.x;
+    const int wave = t / kWave, lane = t & (kWave - 1);
     const int entries = tiles_q + tiles_k;
     for (int e = t; e < entries; e += kSelectThreads)
         factors[e] = amax[static_cast<std::int64_t>(head) * entries + e];
+    // At most 8192 * 8192 tiles (tiles_q + tiles_k <= 16384): counts fit 32 bits.
     const std::int64_t total = static_cast<std::int64_t>(tiles_q) * tiles_k;
     std::uint8_t* out = codes + static_cast<std::int64_t>(head) * total;
-    auto key_of = [&](std::int64_t index) {
-        const float e = factors[index / tiles_k] * factors[tiles_q + index % tiles_k];
-        return __float_as_uint(e);
-    };
-    if (t == 0) still_needed = static_cast<unsigned long long>(count);
+    if (t == 0) still_needed = static_cast<unsigned>(count);
     __syncthreads();
     if (count <= 0 || count >= total) {
         const std::uint8_t code = count <= 0 ? kInt8 : kFp16;
         for (std::int64_t e = t; e < total; e += kSelectThreads) out[e] = code;
         return;
     }
-    unsigned prefix = 0, mask = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int b = t; b < 256; b += kSelectThreads) histogram[b] = 0;
-        __syncthreads();
-        for (std::int64_t e = t; e < total; e += kSelectThreads) {
-            const unsigned key = key_of(e);
-            if ((key & mask) == prefix) atomicAdd(&histogram[(key >> shift) & 255u], 1u);
+    auto key_at = [&](int row, int col) { return __float_as_uint(factors[row] * factors[tiles_q + col]); };
+    // The first tile this thread visits and the fixed step between its tiles.
+    constexpr int kStep = kKeys > 0 ? kWave : kSelectThreads;
+    const int first = kKeys > 0 ? wave * kWave * kKeys + lane : t;
+    const int row0 = first / tiles_k, col0 = first % tiles_k;
+    const int row_step = kStep / tiles_k, col_step = kStep % tiles_k;
+    auto advance = [&](int& row, int& col) {
+        row += row_step;
+        col += col_step;
+        if (col >= tiles_k) {
+            col -= tiles_k;
+            ++row;
         }
-        __syncthreads();
-        if (t == 0) {
-            // Largest digit first: the digit whose bin holds the still-needed rank.
-            unsigned long long above = 0;
-            unsigned digit = 0;
-            for (int b = 255; b >= 0; --b) {
-                if (above + histogram[b] >= still_needed) {
-                    digit = static_cast<unsigned>(b);
-                    break;
-                }
-                above += histogram[b];
+    };
+    // kKeys > 0: total <= 1024 kKeys, so `remaining` (tiles from this
+    // thread's first on) fits an int; slot u is in range when 64 u < remaining.
+    // in_range() hides the value from the compiler so that it recomputes the
+    // comparisons where they are needed instead of holding their lane masks.
+    const int remaining = kKeys > 0 ? static_cast<int>(total) - first : 0;
+    auto in_range = [&]() {
+        int r = remaining;
+        asm volatile("" : "+v"(r));
+        return r;
+    };
+    unsigned keys[kKeys > 0 ? kKeys : 1];
+    unsigned low = ~0u, high = 0u;
+    if constexpr (kKeys > 0) {
+        // (row, column) step from slot to slot; the empty asm keeps the
+        // compiler from re-deriving every slot's column from the first.
+        const int r = in_range();
+        int row = row0, col = col0;
+#pragma unroll
+        for (int u = 0; u < kKeys; ++u) {
+            keys[u] = key_at(min(row, tiles_q - 1), col);
+            const bool valid = u * kWave < r;
+            low = valid ? min(low, keys[u]) : low;
+            high = valid ? max(high, keys[u]) : high;
+            advance(row, col);
+            asm volatile("" : "+v"(row), "+v"(col));
+        }
+    } else {
+        int row = row0, col = col0;
+        for (std::int64_t e = first; e < total; e += kStep) {
+            const unsigned key = key_at(row, col);
+            low = min(low, key);
+            high = max(high, key);
+            advance(row, col);
+        }
+    }
+#pragma unroll
+    for (int offset = 1; offset < kWave; offset <<= 1) {
+        low = min(low, static_cast<unsigned>(__shfl_xor(static_cast<int>(low), offset)));
+        high = max(high, static_cast<unsigned>(__shfl_xor(static_cast<int>(high), offset)));
+    }
+    if (lane == 0) {
+        wave_low[wave] = low;
+        wave_high[wave] = high;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        low = min(low, wave_low[w]);
+        high = max(high, wave_high[w]);
+    }
+    const unsigned smallest = low;
+    if constexpr (kKeys > 0) {
+        const int r = in_range();
+#pragma unroll
+        for (int u = 0; u < kKeys; ++u) keys[u] = u * kWave < r ? keys[u] - smallest : 0u;
+    }
+    // visit(e, key) with key relative to the smallest, for every tile of
+    // this thread (kKeys > 0: also those past the end, which a store leaves out).
+    auto for_each_tile = [&](auto&& visit) {
+        if constexpr (kKeys > 0) {
+#pragma unroll
+            for (int u = 0; u < kKeys; ++u) visit(static_cast<std::int64_t>(first + u * kWave), keys[u]);
+        } else {
+            int row = row0, col = col0;
+            for (std::int64_t e = first; e < total; e += kStep) {
+                visit(e, key_at(row, col) - smallest);
+                advance(row, col);
             }
-            chosen_digit = digit;
-            still_needed -= above;
+        }
+    };
+    // Passes from the top of the range down to bit 0: the first takes up to
+    // kDigitBits bits (the keys are densest there, so the widest histogram
+    // spreads them most), the others split the rest evenly.
+    const unsigned range = high - smallest;
+    const int bits = range ? 32 - __clz(static_cast<int>(range)) : 1;
+    const int passes = (bits + kDigitBits - 1) / kDigitBits;
+    const int first_width = min(bits, kDigitBits);
+    const int width = passes > 1 ? (bits - first_width + passes - 2) / (passes - 1) : first_width;
+    unsigned prefix = 0, mask = 0;
+    int shift = bits;
+    for (int pass = 0; pass < passes; ++pass) {
+        const int next = max(shift - (pass == 0 ? first_width : width), 0);
+        const unsigned digits = shift - next;
+        for (int b = t; b < kBins; b += kSelectThreads) histogram[b] = 0;
+        __syncthreads();
+        for_each_tile([&](std::int64_t, unsigned key) {
+            if ((key & mask) == prefix) atomicAdd(&histogram[__builtin_amdgcn_ubfe(key, next, digits)], 1u);
+        });
+        const unsigned need = still_needed;
+        __syncthreads();
+        // Thread t holds bins kBins - 1 - 2t and kBins - 2 - 2t (largest
+        // first); a scan over threads counts the keys above each thread's
+        // bins, and the thread whose bins reach the still-needed rank picks.
+        const unsigned top = histogram[kBins - 1 - 2 * t], below_top = histogram[kBins - 2 - 2 * t];
+        const unsigned sum = top + below_top;
+        unsigned inclusive = sum;
+#pragma unroll
+        for (int offset = 1; offset < kWave; offset <<= 1) {
+            const unsigned up = __shfl_up(inclusive, offset);
+            if (lane >= offset) inclusive += up;
+        }
+        if (lane == kWave - 1) wave_low[wave] = inclusive;
+        __syncthreads();
+        unsigned above = inclusive - sum;
+        for (int w = 0; w < wave; ++w) above += wave_low[w];
+        if (above < need && above + sum >= need) {
+            const bool in_top = above + top >= need;
+            chosen_digit = static_cast<unsigned>(in_top ? kBins - 1 - 2 * t : kBins - 2 - 2 * t);
+            still_needed = in_top ? need - above : need - above - top;
+            equal_keys = in_top ? top : below_top;
         }
         __syncthreads();
-        prefix |= chosen_digit << shift;
-        mask |= 255u << shift;
+        prefix |= chosen_digit << next;
+        mask |= ((1u << digits) - 1u) << next;
+        shift = next;
     }
     // prefix = the count-th largest key; still_needed = how many of the keys
-    // equal to it are FP16 (the lowest indices).
-    const unsigned long long ties = still_needed;
-    unsigned long long ties_before = 0;
-    for (std::int64_t base = 0; base < total; base += kSelectThreads) {
-        const std::int64_t e = base + t;
-        const unsigned key = e < total ? key_of(e) : 0u;
-        const unsigned equal = (e < total && key == prefix) ? 1u : 0u;
-        scan[t] = equal;
-        __syncthreads();
-        // Inclusive scan (Hillis-Steele) of the tie flags in index order.
-        for (int offset = 1; offset < kSelectThreads; offset <<= 1) {
-            const unsigned add = t >= offset ? scan[t - offset] : 0u;
-            __syncthreads();
-            scan[t] += add;
-            __syncthreads();
+    // equal to it are FP16 (the lowest indices), equal_keys how many there are.
+    const unsigned ties = still_needed;
+    if (ties == equal_keys) {
+        if constexpr (kKeys > 0) {
+            const int r = in_range();
+#pragma unroll
+            for (int u = 0; u < kKeys; ++u)
+                if (u * kWave < r) out[first + u * kWave] = keys[u] >= prefix ? kFp16 : kInt8;
+        } else {
+            for_each_tile([&](std::int64_t e, unsigned key) { out[e] = key >= prefix ? kFp16 : kInt8; });
         }
-        if (e < total) {
-            const unsigned long long rank = ties_before + scan[t] - equal;
-            out[e] = (key > prefix || (equal && rank < ties)) ? kFp16 : kInt8;
-        }
-        ties_before += scan[kSelectThreads - 1];
+        return;
+    }
+    auto lanes_below = [&](unsigned long long ballot) {
+        return __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(ballot >> 32),
+                                         __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(ballot), 0u));
+    };
+    if constexpr (kKeys > 0) {
+        unsigned mine = 0;
+#pragma unroll
+        for (int u = 0; u < kKeys; ++u) mine += static_cast<unsigned>(__popcll(__ballot(keys[u] == prefix)));
+        if (lane == 0) wave_low[wave] = mine;
         __syncthreads();
+        unsigned before = 0;
+        for (int w = 0; w < wave; ++w) before += wave_low[w];
+        const int r = in_range();
+#pragma unroll
+        for (int u = 0; u < kKeys; ++u) {
+            const bool equal = keys[u] == prefix;
+            const unsigned long long ballot = __ballot(equal);
+            if (u * kWave < r)
+                out[first + u * kWave] =
+                    (keys[u] > prefix || (equal && before + lanes_below(ballot) < ties)) ? kFp16 : kInt8;
+            before += static_cast<unsigned>(__popcll(ballot));
+        }
+    } else {
+        // Chunk by chunk of 1024 tiles: ties before this one are those of
+        // earlier chunks, earlier waves and earlier lanes.
+        unsigned ties_before = 0;
+        int row = row0, col = col0;
+        for (std::int64_t base = 0; base < total; base += kSelectThreads) {
+            const std::int64_t e = base + t;
+            const unsigned key = e < total ? key_at(row, col) - smallest : 0u;
+            const bool equal = e < total && key == prefix;
+            const unsigned long long ballot = __ballot(equal);
+            if (lane == 0) wave_low[wave] = static_cast<unsigned>(__popcll(ballot));
+            __syncthreads();
+            unsigned earlier = 0, all = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                earlier += w < wave ? wave_low[w] : 0u;
+                all += wave_low[w];
+            }
+            if (e < total)
+                out[e] = (key > prefix || (equal && ties_before + earlier + lanes_below(ballot) < ties)) ? kFp16
+                                                                                                        : kInt8;
+            ties_before += all;
+            __syncthreads();
+            advance(row, col);
+        }
     }
 }
 
-// One thread per output word: bit b of word w of query tile qt is group
-// 64w + b, whose key tiles lie in coarse tile (kt * 32) / tile_keys.
-__global__ void pack_kernel(const std::uint8_t* codes, int heads, int q_tiles16, int words_per_row, int groups,
-                            int key_tiles_per_group, int tiles_q, int tiles_k, int tile_rows, int tile_keys,
-                            std::uint64_t* route_words, std::uint64_t* skip_words) {
-    const std::int64_t total = static_cast<std::int64_t>(heads) * q_tiles16 * words_per_row;
-    const std::int64_t t = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (t >= total) return;
-    const int w = static_cast<int>(t % words_per_row);
-    const int qt = static_cast<int>((t / words_per_row) % q_tiles16);
-    const std::int64_t head = t / (static_cast<std::int64_t>(words_per_row) * q_tiles16);
-    const int i = qt * kCellRows / tile_rows;
-    const std::uint8_t* row = codes + (head * tiles_q + i) * tiles_k;
-    std::uint64_t route = 0, skip = 0;
-    for (int b = 0; b < 64; ++b) {
-        const int group = 64 * w + b;
-        if (group >= groups) break;
-        const std::int64_t kt = static_cast<std::int64_t>(group) * key_tiles_per_group;
-        const std::uint8_t code = row[kt * kCellKeys / tile_keys];
-        route |= static_cast<std::uint64_t>(code == kInt8) << b;
-        skip |= static_cast<std::uint64_t>(code == kSkip) << b;
+// One wave per (head, coarse tile row i): bit b of word w is group 64w + b,
+// whose key tiles lie in coarse tile (kt * 32) / tile_keys; lane b reads
+// that code and two ballots form the route and skip words. Every 16-row
+// query tile the coarse row covers gets the same words, so the wave computes
+// them once and its lanes store the copies.
+__global__ __launch_bounds__(256) void pack_kernel(const std::uint8_t* codes, int heads, int q_tiles16,
+                                                   int words_per_row, int groups, int key_tiles_per_group,
+                                                   int tiles_q, int tiles_k, int tile_rows, int tile_keys,
+                                                   std::uint64_t* route_words, std::uint64_t* skip_words) {
+    const std::int64_t wave = (static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (wave >= static_cast<std::int64_t>(heads) * tiles_q) return;  // whole waves
+    const std::int64_t head = wave / tiles_q;
+    const int i = static_cast<int>(wave % tiles_q);
+    const std::uint8_t* row = codes + wave * tiles_k;
+    const int qt0 = i * (tile_rows / kCellRows);
+    const int copies = min(tile_rows / kCellRows, q_tiles16 - qt0);
+    const std::int64_t out = (head * q_tiles16 + qt0) * words_per_row;
+    for (int w = 0; w < words_per_row; ++w) {
+        const int group = 64 * w + lane;
+        std::uint8_t code = kFp16;
+        if (group < groups) {
+            const std::int64_t kt = static_cast<std::int64_t>(group) * key_tiles_per_group;
+            code = row[kt * kCellKeys / tile_keys];
+        }
+        const std::uint64_t route = __ballot(code == kInt8);
+        const std::uint64_t skip = __ballot(code == kSkip);
+        for (int r = lane; r < copies; r += kWave) {
+            route_words[out + static_cast<std::int64_t>(r) * words_per_row + w] = route;
+            skip_words[out + static_cast<std::int64_t>(r) * words_per_row + w] = skip;
+        }
     }
-    route_words[t] = route;
-    skip_words[t] = skip;
 }
 
 unsigned blocks_for(std::int64_t items, int threads) {
@@ -267,9 +474,10 @@ extern "C" int tilemix_routes_from_tiles(const std::uint8_t* tile_codes, int hea
     const int groups = (key_tiles32 - 1) / key_tiles_per_group + 1;
     const int words_per_row = (groups - 1) / 64 + 1;
     const std::int64_t words = static_cast<std::int64_t>(heads) * q_tiles16 * words_per_row;
-    if (!grid_ok(words, 256)) return hipErrorInvalidConfiguration;
     const int tiles_q = (M - 1) / tile_rows + 1, tiles_k = (N - 1) / tile_keys + 1;
-    pack_kernel<<<blocks_for(words, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+    const std::int64_t lanes = static_cast<std::int64_t>(heads) * tiles_q * kWave;
+    if (!grid_ok(words, 256) || !grid_ok(lanes, 256)) return hipErrorInvalidConfiguration;
+    pack_kernel<<<blocks_for(lanes, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
         tile_codes, heads, q_tiles16, words_per_row, groups, key_tiles_per_group, tiles_q, tiles_k, tile_rows,
         tile_keys, route_words, skip_words);
     return hipGetLastError();
@@ -385,13 +593,26 @@ hipError_t launch_importance(const std::uint16_t* Q, const std::uint16_t* K, int
     const std::int64_t count = static_cast<std::int64_t>(std::nearbyint(static_cast<double>(fp16_fraction) * total));
     const std::int64_t qs = heads > 1 ? q_head_stride : static_cast<std::int64_t>(M) * d;
     const std::int64_t ks = heads > 1 ? k_head_stride : static_cast<std::int64_t>(N) * d;
-    tile_absmax_kernel<<<dim3(static_cast<unsigned>(tiles_q + tiles_k), static_cast<unsigned>(heads)), 256, 0, s>>>(
-        Q, K, M, N, d, qs, ks, tiles_q, tiles_k, tile_rows, tile_keys, workspace);
+    const dim3 grid(static_cast<unsigned>(tiles_q + tiles_k), static_cast<unsigned>(heads));
+    const bool vector = d % 8 == 0 && reinterpret_cast<std::uintptr_t>(Q) % 16 == 0 &&
+                        reinterpret_cast<std::uintptr_t>(K) % 16 == 0 && (qs * 2) % 16 == 0 && (ks * 2) % 16 == 0;
+    if (vector)
+        tile_absmax_kernel<true><<<grid, 256, 0, s>>>(Q, K, M, N, d, qs, ks, tiles_q, tiles_k, tile_rows, tile_keys,
+                                                      workspace);
+    else
+        tile_absmax_kernel<false><<<grid, 256, 0, s>>>(Q, K, M, N, d, qs, ks, tiles_q, tiles_k, tile_rows, tile_keys,
+                                                       workspace);
     hipError_t status = hipGetLastError();
     if (status != hipSuccess) return status;
-    importance_select_kernel<<<static_cast<unsigned>(heads), kSelectThreads,
-                               static_cast<std::size_t>(tiles_q + tiles_k) * sizeof(float), s>>>(
-        workspace, tiles_q, tiles_k, count, tile_codes);
+    const std::size_t lds = static_cast<std::size_t>(tiles_q + tiles_k) * sizeof(float);
+    const unsigned blocks = static_cast<unsigned>(heads);
+    if (total <= 8 * kSelectThreads)
+        importance_select_kernel<8><<<blocks, kSelectThreads, lds, s>>>(workspace, tiles_q, tiles_k, count, tile_codes);
+    else if (total <= 32 * kSelectThreads)
+        importance_select_kernel<32><<<blocks, kSelectThreads, lds, s>>>(workspace, tiles_q, tiles_k, count,
+                                                                          tile_codes);
+    else
+        importance_select_kernel<0><<<blocks, kSelectThreads, lds, s>>>(workspace, tiles_q, tiles_k, count, tile_codes);
     return hipGetLastError();
 }
 
