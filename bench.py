@@ -30,9 +30,14 @@ more untimed steps run (``roofline.sclk_mhz_sampled``). The MFMA peaks are
 quoted at 2.4 GHz; with N(0,1) operands the card holds a lower clock under its
 power limit (``--input-scale 0`` shows the same kernel at 2.4 GHz).
 
+``--ceiling`` runs tests/native/_build/ceiling_probe instead and prints its
+lines: the sustained MFMA rate against operand data (zeros against random
+fp16 / int8: the power limit), the LDS fragment-read rates, and the kernel's
+MFMA phases with zero operands (near 2.4 GHz).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--min-warmup-ms T] [--config 3]
                        [--precise] [--no-check] [--no-cpu-baseline] [--no-clock]
-                       [--input-scale F]
+                       [--input-scale F] [--ceiling]
 """
 from __future__ import annotations
 
@@ -85,6 +90,8 @@ def parse_args():
                         "'demo' = the reference demo workload (M=1000 N=1003 d=128, g=2, mask 0xaaaa...), "
                         "'config' = a loop of per-head calls over --config's heads (no causal mask or "
                         "skip in that API: every pair is computed, skipped cells as FP16)")
+    p.add_argument("--ceiling", action="store_true",
+                   help="run the hardware-ceiling probe (tests/native/ceiling_probe.hip) instead")
     return p.parse_args()
 
 
@@ -99,6 +106,15 @@ def main() -> int:
                           "across GPUs by head with no exchange between them, but multi-GPU runs are "
                           "not part of this build; run with --gpus 1"}))
         return 2
+
+    if args.ceiling:
+        import subprocess
+
+        probe = ROOT / "tests" / "native" / "_build" / "ceiling_probe"
+        if not probe.exists():
+            print(json.dumps({"error": f"{probe} is not built; run python tests/native/build.py"}))
+            return 1
+        return subprocess.run([str(probe)]).returncode
 
     import torch
     import tilemix
