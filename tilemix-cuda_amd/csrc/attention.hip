@@ -31,10 +31,11 @@
 //    computed once, each tile only changes a scalar offset, and rows past
 //    the end of the head read as zero. Every wave issues the same number of
 //    loads per buffer (spare slots read out of range into a 1 KiB landing
-//    area), so the issue code has no branches. The V tile is fetched while
-//    the scores are computed and the next K tile while softmax and P.V run,
-//    with two barriers per tile; at d = 128, 40 KiB of tile buffers plus
-//    18 KiB of quantized Q rows let two workgroups share a CU.
+//    area), so the issue code has no branches. V has two buffers, K and K8
+//    one each: the next tile's K, K8 and V are all fetched after the tile's
+//    second barrier, while softmax and P.V run, so no tile load is issued
+//    among the score MFMAs; two barriers per tile. At d = 128, 56 KiB of tile
+//    buffers plus 18 KiB of quantized Q rows let two workgroups share a CU.
 //  * Each SIMD runs one wave of each of the CU's two workgroups. A tile is an
 //    MFMA phase (P.V, barrier, next scores) and a VALU phase (softmax). A
 //    wave's issue priority is low in the first half of each phase and high
@@ -97,7 +98,9 @@ struct Layout {
     static constexpr int kK8PerWave = (kK8Loads + kWavesPerGroup - 1) / kWavesPerGroup;
     static constexpr int kQ8Stride = kDP8 + 16;    // the workgroup's quantized Q rows
     static constexpr int kQ8Bytes = kRowsPerGroup * kQ8Stride;
-    static constexpr int kSmemBytes = kKBytes + kVBytes + kK8Bytes;
+    // K, V buffer 0, K8, V buffer 1.
+    static constexpr int kV1Offset = kVBytes + kK8Bytes;  // V buffer 1 - V buffer 0
+    static constexpr int kSmemBytes = kKBytes + kVBytes + kK8Bytes + kVBytes;
     static_assert(kKBytes % 1024 == 0 && kVBytes % 1024 == 0 && kK8Bytes % 1024 == 0,
                   "tiles are whole wave loads");
     // Chunk rotation of a rotated row of kChunks 16-byte chunks. Key rows
@@ -521,12 +524,15 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             for (int t = 0; t < L::kK8PerWave; ++t) load_to_lds(r, dst_k8[t], off_k8[t], soffset);
         }
     };
-    auto v_slots = [&](int4v r, int soffset) {
+    // V into buffer `buffer` (0 or 1); spare slots keep their landing area.
+    auto v_slots = [&](int4v r, int soffset, int buffer) {
+        const unsigned shift = buffer ? static_cast<unsigned>(L::kV1Offset) : 0u;
         if constexpr (L::kVLoads % kWavesPerGroup == 0) {
-            load_slots(r, dst_v[0], off_v, soffset);
+            load_slots(r, dst_v[0] + shift, off_v, soffset);
         } else {
 #pragma unroll
-            for (int t = 0; t < L::kVPerWave; ++t) load_to_lds(r, dst_v[t], off_v[t], soffset);
+            for (int t = 0; t < L::kVPerWave; ++t)
+                load_to_lds(r, dst_v[t] == lds_spare_address ? dst_v[t] : dst_v[t] + shift, off_v[t], soffset);
         }
     };
     // K (FP16 cells) and K8 (INT8 cells) of tile j.
@@ -559,15 +565,16 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             }
         }
     };
-    auto issue_v = [&](int j) {
+    auto issue_v = [&](int j, int buffer) {
         const int k0 = j * kTileKeys;
         if constexpr (kVector) {
-            if (k0 + kTileKeys > N) v_slots(rsrc_from(rsrc_v, k0 * v_row_bytes), 0);
-            else v_slots(rsrc_v, k0 * v_row_bytes);
+            if (k0 + kTileKeys > N) v_slots(rsrc_from(rsrc_v, k0 * v_row_bytes), 0, buffer);
+            else v_slots(rsrc_v, k0 * v_row_bytes, buffer);
         } else {
+            unsigned char* const dst = lds_v + (buffer ? L::kV1Offset : 0);
             for (int e = tid; e < kTileKeys * kDP; e += kThreadsPerGroup) {
                 const int row = e / kDP, f = e % kDP, key = k0 + row;
-                *reinterpret_cast<std::uint16_t*>(lds_v + L::v_at(row, 2 * f)) =
+                *reinterpret_cast<std::uint16_t*>(dst + L::v_at(row, 2 * f)) =
                     (key < N && f < d) ? Vh[static_cast<std::int64_t>(key) * p.v_row + f] : 0;
             }
         }
@@ -637,8 +644,16 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         }
         return j;
     };
+    // Tile j's V sits in buffer v_buffer. The loads of the next visible tile
+    // (K, K8, and V into the other buffer) are issued after the tile's second
+    // barrier: by then every wave has finished its scores (the K and K8
+    // buffers are free) and the previous tile's P.V (its V buffer is free).
     int j = next_tile(0);
-    if (j < tiles) issue_k(j, needs16(cur_int8, cur_skip), cur_int8 != 0);
+    int v_buffer = 0;
+    if (j < tiles) {
+        issue_k(j, needs16(cur_int8, cur_skip), cur_int8 != 0);
+        issue_v(j, v_buffer);
+    }
 
     // One iteration per visible tile. A wave with no visible key in the tile
     // (rows above a causal diagonal, or all its cells skipped) takes part in
@@ -647,9 +662,8 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     while (j < tiles) {
         const int k0 = j * kTileKeys;
         const std::uint32_t int8_mask = cur_int8, skip_mask = cur_skip;
-        tile_barrier();  // K_j landed; every wave finished P.V of the previous tile
+        tile_barrier();  // K_j, V_j landed; every wave finished P.V of the previous tile
         set_priority<2>();  // second half of the MFMA phase (P.V, then these scores)
-        issue_v(j);
 
         const unsigned wave_int8 = (int8_mask >> (4 * wave)) & 0xfu;
         const unsigned wave_skip = (skip_mask >> (4 * wave)) & 0xfu;
@@ -789,10 +803,13 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         }
 
 
-        tile_barrier();  // V_j landed; every wave finished reading K_j
+        tile_barrier();  // every wave finished reading K_j (and P.V of the previous tile)
         set_priority<0>();  // first half of the VALU phase
         const int j_next = next_tile(j + 1);
-        if (j_next < tiles) issue_k(j_next, needs16(cur_int8, cur_skip), cur_int8 != 0);
+        if (j_next < tiles) {
+            issue_k(j_next, needs16(cur_int8, cur_skip), cur_int8 != 0);
+            issue_v(j_next, v_buffer ^ 1);
+        }
 
         // ---- online softmax, then O^T += V^T P^T
         if (active) {
@@ -802,7 +819,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 // V^T fragment of step t = (key step t / kOB, feature block
                 // t % kOB), read kAhead steps before its MFMA.
                 auto v_frag = [&](int t) {
-                    const unsigned char* v_lo = lds_v + 16 * L::kVStride * (t / kOB) + v_lane[t % kOB];
+                    const unsigned char* v_lo = lds_v + (v_buffer ? L::kV1Offset : 0) + 16 * L::kVStride * (t / kOB) + v_lane[t % kOB];
                     return concat(read_tr16(v_lo), read_tr16(v_lo + 8 * L::kVStride));
                 };
                 constexpr int kSteps = 4 * kOB;
@@ -824,6 +841,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             }
         }
         j = j_next;
+        v_buffer ^= 1;
     }
 
     // Routing trace of tiles a causal workgroup never visits.
