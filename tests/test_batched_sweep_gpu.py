@@ -2,7 +2,8 @@
 against the fp64 TileMix oracle.
 
 The hand-picked cases of test_batched_gpu.py fix one option set each; here 24
-cases drawn once from a fixed seed combine them: 1-3 heads, ragged M and N,
+cases drawn once from a fixed seed combine them (and 8 more with rows of up to
+3200 keys): 1-3 heads, ragged M and N,
 d from 1 to 128, key_tiles_per_group 1-5, causal or not, skip routes or not,
 quantize mode 0 (Q8/K8 given), 1 (both quantized here) or 2 (K8 given, Q
 quantized in the kernel), fast or precise P.V, O 16-byte aligned or not, and
@@ -26,17 +27,24 @@ MAX_ABS, MEAN_ABS = 2e-3, 2e-4
 PAD = 64
 
 
+def _draw(rng, d, max_m, max_n):
+    return dict(
+        heads=int(rng.integers(1, 4)), M=int(rng.integers(1, max_m)), N=int(rng.integers(1, max_n)),
+        d=d, g=int(rng.choice([1, 2, 3, 5])), causal=bool(rng.random() < 0.5),
+        p_skip=float(rng.choice([0.0, 0.25])), quantize=int(rng.integers(0, 3)),
+        precise=bool(rng.random() < 0.5), aligned=bool(rng.random() < 0.5),
+        scale_kind=str(rng.choice(["pos", "pos", "pos", "zero", "neg"])))
+
+
 def _cases():
     rng = np.random.default_rng(20261202)
     dims = [1, 7, 16, 24, 40, 64, 72, 96, 100, 120, 128]
-    cases = []
-    for i in range(24):  # every head dimension at least twice, the other options drawn
-        cases.append(dict(
-            heads=int(rng.integers(1, 4)), M=int(rng.integers(1, 700)), N=int(rng.integers(1, 900)),
-            d=dims[i % len(dims)], g=int(rng.choice([1, 2, 3, 5])), causal=bool(rng.random() < 0.5),
-            p_skip=float(rng.choice([0.0, 0.25])), quantize=int(rng.integers(0, 3)),
-            precise=bool(rng.random() < 0.5), aligned=bool(rng.random() < 0.5),
-            scale_kind=str(rng.choice(["pos", "pos", "pos", "zero", "neg"]))))
+    # every head dimension at least twice, the other options drawn
+    cases = [_draw(rng, dims[i % len(dims)], 700, 900) for i in range(24)]
+    # Long rows (up to 50 key tiles): the kernel alternates two V buffers per
+    # visited tile and steps over skipped tiles, over many tiles per workgroup.
+    long_rng = np.random.default_rng(20261203)
+    cases += [_draw(long_rng, [64, 96, 128, 128][i % 4], 3000, 3200) for i in range(8)]
     return cases
 
 
