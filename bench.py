@@ -25,19 +25,16 @@ headline attention launch goes from about 0.39 ms to 0.31 ms after roughly
 rate. The JSON line reports W as requested and the steps actually run; the
 timed region is exactly K steps either way.
 
-The warm-up ends with a shader-clock sample: rocm-smi reads the clock while
-more untimed steps run (``roofline.sclk_mhz_sampled``). The MFMA peaks are
-quoted at 2.4 GHz; with N(0,1) operands the card holds a lower clock under its
-power limit (``--input-scale 0`` shows the same kernel at 2.4 GHz).
-
-``--ceiling`` runs tests/native/_build/ceiling_probe instead and prints its
-lines: the sustained MFMA rate against operand data (zeros against random
-fp16 / int8: the power limit), the LDS fragment-read rates, and the kernel's
-MFMA phases with zero operands (near 2.4 GHz).
+After the timed steps, the card's `pp_dpm_sclk` sysfs file is read while more untimed
+steps run (``roofline.sclk_mhz_sampled``; plain file reads, no child process). Reading
+the clock level slows the following launches for a while, so the sample never precedes
+the timed region. The MFMA peaks are quoted at 2.4 GHz; with N(0,1) operands the card
+holds a lower clock under its power limit (``--input-scale 0`` shows the same kernel at
+2.4 GHz).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--min-warmup-ms T] [--config 3]
                        [--precise] [--no-check] [--no-cpu-baseline] [--no-clock]
-                       [--input-scale F] [--ceiling]
+                       [--input-scale F] [--routing] [--per-head demo|config]
 """
 from __future__ import annotations
 
@@ -77,7 +74,7 @@ def parse_args():
                    help="after timing, run one device copy of this many MiB on the bench stream "
                         "(calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE against known bytes)")
     p.add_argument("--no-clock", action="store_true",
-                   help="skip the rocm-smi shader-clock sample taken after the timed steps")
+                   help="skip the sysfs shader-clock sample taken after the timed steps")
     p.add_argument("--input-scale", type=float, default=1.0,
                    help="diagnostic: multiply Q, K and V by this factor after the routing codes are "
                         "drawn from the unscaled inputs (same routes, same INT8 codes, smaller "
@@ -90,8 +87,6 @@ def parse_args():
                         "'demo' = the reference demo workload (M=1000 N=1003 d=128, g=2, mask 0xaaaa...), "
                         "'config' = a loop of per-head calls over --config's heads (no causal mask or "
                         "skip in that API: every pair is computed, skipped cells as FP16)")
-    p.add_argument("--ceiling", action="store_true",
-                   help="run the hardware-ceiling probe (tests/native/ceiling_probe.hip) instead")
     return p.parse_args()
 
 
@@ -106,15 +101,6 @@ def main() -> int:
                           "across GPUs by head with no exchange between them, but multi-GPU runs are "
                           "not part of this build; run with --gpus 1"}))
         return 2
-
-    if args.ceiling:
-        import subprocess
-
-        probe = ROOT / "tests" / "native" / "_build" / "ceiling_probe"
-        if not probe.exists():
-            print(json.dumps({"error": f"{probe} is not built; run python tests/native/build.py"}))
-            return 1
-        return subprocess.run([str(probe)]).returncode
 
     import torch
     import tilemix
@@ -172,12 +158,6 @@ def main() -> int:
                 step()
             warmup_run += 8
             torch.cuda.synchronize()
-        # The shader clock under sustained load, sampled while more untimed steps run.
-        sclk = None
-        if not args.no_clock:
-            sclk, sample_steps = sample_sclk_mhz(step, torch.cuda.synchronize)
-            warmup_run += sample_steps
-            log(f"sampled shader clock: {sclk} MHz")
         warmup_ms = (time.perf_counter() - warm_start) * 1e3
         log(f"warm-up: {warmup_run} steps in {warmup_ms:.1f} ms ({args.warmup} requested, "
             f"minimum {args.min_warmup_ms:g} ms)")
@@ -189,6 +169,13 @@ def main() -> int:
             step(pairs[k])
         torch.cuda.synchronize()
         t1 = time.perf_counter()
+        # The shader clock under sustained load, sampled while more untimed steps run after
+        # the timed ones: reading the clock level slows the kernel for a while (measured: the
+        # next 20 steps about 20 % slower), so it never precedes the timed region.
+        sclk = None
+        if not args.no_clock:
+            sclk, sample_steps = sample_sclk_mhz(step, torch.cuda.synchronize)
+            log(f"sampled shader clock: {sclk} MHz ({sample_steps} untimed steps after the timed ones)")
         if args.copy_probe_mib > 0:
             src = torch.ones(args.copy_probe_mib << 19, dtype=torch.float16, device=dev)
             dst = torch.empty_like(src)
@@ -371,7 +358,7 @@ def per_head_bench(args) -> dict:
         # src/main.cu:22-58: M=1000, N=1003, d=128, key_tiles_per_group 2, every routing word
         # 0xaaaa... (odd 64-key groups INT8, even ones FP16), inputs periodic in the index.
         M, N, d, g, heads = 1000, 1003, 128, 2, 1
-        # The demo's periodic inputs (periods 17, 19, 23; examples/demo_main.cpp).
+        # The demo's periodic inputs (periods 17, 19, 23; src/main.cu:38-40).
         idx = torch.arange(max(M, N) * d, dtype=torch.int64)
         Q = (0.125 * ((idx[: M * d] % 17) - 8).float()).to(torch.float16).reshape(1, M, d).to(dev)
         K = (0.125 * ((idx[: N * d] % 19) - 9).float()).to(torch.float16).reshape(1, N, d).to(dev)
@@ -457,55 +444,68 @@ def source_stamp() -> str:
     return h.hexdigest()[:16]
 
 
-def parse_sclk_csv(text: str) -> float | None:
-    """The shader clock in MHz from `rocm-smi --showclocks --csv` output (header row starting
-    'device' with a 'sclk clock speed:' column, then one row per card, e.g. '(2040Mhz)'), or
-    None when the layout is not that one."""
-    lines = [line.strip() for line in text.splitlines() if line.strip()]
-    header = next((line for line in lines if line.startswith("device")), None)
-    row = next((line for line in lines if line.startswith("card")), None)
-    if header is None or row is None:
-        return None
-    columns = header.split(",")
-    if "sclk clock speed:" not in columns:
-        return None
-    fields = row.split(",")
-    index = columns.index("sclk clock speed:")
-    if index >= len(fields):
-        return None
-    digits = "".join(ch for ch in fields[index] if ch.isdigit() or ch == ".")
-    return float(digits) if digits else None
+def parse_dpm_sclk(text: str) -> float | None:
+    """The current shader clock in MHz from an amdgpu `pp_dpm_sclk` sysfs file: one line per
+    clock level ("0: 500Mhz", "1: 2100Mhz *"), the level in use marked with '*'. None when no
+    line is marked or the marked line carries no number."""
+    for line in text.splitlines():
+        if line.rstrip().endswith("*"):
+            _, _, level = line.partition(":")
+            digits = "".join(ch for ch in level if ch.isdigit() or ch == ".")
+            return float(digits) if digits else None
+    return None
 
 
-def sample_sclk_mhz(step, sync) -> tuple[float | None, int]:
-    """Shader clock (MHz) that rocm-smi reports while bench steps keep the GPU busy (None when
-    rocm-smi is unavailable), and the number of steps run meanwhile. The MI355X holds its 2.4 GHz maximum only while it is under
-    its power limit; with N(0,1) operands this kernel runs below it (zero operands: at it)."""
-    import subprocess
+def sclk_files(device: int = 0) -> list[Path]:
+    """The `pp_dpm_sclk` file of torch device `device`, found through its PCI address; when the
+    address is unknown, the only such file under /sys/class/drm (several cards: none)."""
+    try:
+        import torch
+
+        props = torch.cuda.get_device_properties(device)
+        pattern = f"{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:{props.pci_device_id:02x}.*"
+        found = sorted(Path("/sys/bus/pci/devices").glob(f"{pattern}/pp_dpm_sclk"))
+        if found:
+            return found[:1]
+    except Exception:  # no torch device properties, no sysfs
+        pass
+    cards = sorted(Path("/sys/class/drm").glob("card*/device/pp_dpm_sclk"))
+    return cards if len(cards) == 1 else []
+
+
+def sample_sclk_mhz(step, sync, files: list[Path] | None = None, reads: int = 5) -> tuple[float | None, int]:
+    """Shader clock (MHz) read from sysfs while bench steps keep the GPU busy, and the number of
+    steps run meanwhile. The median of `reads` reads of the card's `pp_dpm_sclk` (plain file
+    reads on a helper thread: this process starts no other program, which would be an exec
+    from a process that has initialised the GPU), or None when the file is missing or
+    unreadable. The MI355X holds its 2.4 GHz maximum only while it is under its power limit;
+    with N(0,1) operands this kernel runs below it (zero operands: at it)."""
     import threading
 
-    reading: dict = {}
+    paths = sclk_files() if files is None else files
+    readings: list[float] = []
 
     def read():
-        time.sleep(0.2)
-        try:
-            r = subprocess.run(["rocm-smi", "--showclocks", "--csv"], capture_output=True, text=True,
-                               timeout=20)
-            reading["mhz"] = parse_sclk_csv(r.stdout)
-        except Exception:  # no rocm-smi, no permission
-            pass
+        for _ in range(reads):
+            time.sleep(0.1)
+            try:
+                mhz = parse_dpm_sclk(paths[0].read_text())
+            except (OSError, IndexError):
+                return
+            if mhz is not None:
+                readings.append(mhz)
 
     reader = threading.Thread(target=read, daemon=True)
     reader.start()
     start = time.perf_counter()
     steps = 0
-    while reader.is_alive() and time.perf_counter() - start < 25.0:
+    while reader.is_alive() and time.perf_counter() - start < 5.0:
         for _ in range(8):
             step()
         steps += 8
         sync()
     reader.join(timeout=1.0)
-    return reading.get("mhz"), steps
+    return (float(np.median(readings)) if readings else None), steps
 
 
 def measured_traffic(workload: str):

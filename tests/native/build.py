@@ -6,9 +6,6 @@
 * quant_division_check runs the quantizer's division-free quotient against
   IEEE division for every fp16 (block maximum, value) pair, compiled with the
   library's own device flags.
-* ceiling_probe measures the hardware rates that bound the attention kernel
-  (sustained MFMA rate against operand data, LDS fragment-read rates, the
-  kernel's MFMA phases at full clock); bench.py --ceiling runs it.
 
 Usage: python tests/native/build.py
 """
@@ -25,7 +22,6 @@ ROOT = HERE.parent.parent
 OUT = HERE / "_build"
 EXE = OUT / "tilemix_test"
 DIVISION_CHECK = OUT / "quant_division_check"
-CEILING_PROBE = OUT / "ceiling_probe"
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
 
@@ -49,7 +45,6 @@ def build() -> Path:
           "-o", str(tmp)])
     os.replace(tmp, EXE)
     build_division_check()
-    build_ceiling_probe()
     return EXE
 
 
@@ -68,16 +63,6 @@ def build_division_check() -> Path:
           f"-I{library_build.CSRC}", str(HERE / "quant_division_check.hip"), "-o", str(tmp)])
     os.replace(tmp, DIVISION_CHECK)
     return DIVISION_CHECK
-
-
-def build_ceiling_probe() -> Path:
-    library_build = _library_build()
-    OUT.mkdir(parents=True, exist_ok=True)
-    tmp = CEILING_PROBE.with_suffix(".tmp")
-    _run([HIPCC, *[f for f in library_build.DEVICE_FLAGS if f != "-fPIC"], str(HERE / "ceiling_probe.hip"),
-          "-o", str(tmp)])
-    os.replace(tmp, CEILING_PROBE)
-    return CEILING_PROBE
 
 
 if __name__ == "__main__":

@@ -195,10 +195,7 @@ def test_bench_refuses_more_than_one_gpu():
     assert "one GPU" in line["error"]
 
 
-def test_bench_reads_the_shader_clock_from_rocm_smi_csv():
-    """bench.py's clock sample parses `rocm-smi --showclocks --csv` as printed on the
-    MI355X box (header row, then one row per card), and returns None for any other
-    layout rather than a wrong number."""
+def _bench_module():
     import importlib.util
     from pathlib import Path
 
@@ -206,10 +203,52 @@ def test_bench_reads_the_shader_clock_from_rocm_smi_csv():
     spec = importlib.util.spec_from_file_location("bench_module", root / "bench.py")
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
-    seen = ("device,mclk clock speed:,mclk clock level:,sclk clock speed:,sclk clock level:\n"
-            "card0,(2000Mhz),0,(2040Mhz),1\n")
-    assert bench.parse_sclk_csv(seen) == 2040.0
-    assert bench.parse_sclk_csv("\n" + seen + "\n") == 2040.0
-    assert bench.parse_sclk_csv("device,mclk clock speed:\ncard0,(2000Mhz)\n") is None
-    assert bench.parse_sclk_csv("device,sclk clock speed:\ncard0,()\n") is None
-    assert bench.parse_sclk_csv("") is None
+    return bench
+
+
+def test_bench_parses_the_dpm_sclk_sysfs_file():
+    """bench.py reads the shader clock from the card's `pp_dpm_sclk` file, whose level
+    in use is marked with '*' (amdgpu sysfs layout), and returns None for a file with no
+    marked level rather than a wrong number."""
+    bench = _bench_module()
+    assert bench.parse_dpm_sclk("0: 500Mhz\n1: 2040Mhz *\n2: 2400Mhz\n") == 2040.0
+    assert bench.parse_dpm_sclk("0: 500Mhz *\n1: 2400Mhz\n") == 500.0
+    assert bench.parse_dpm_sclk("0: 500Mhz\n1: 2400Mhz\n") is None
+    assert bench.parse_dpm_sclk("S: *\n") is None
+    assert bench.parse_dpm_sclk("") is None
+
+
+def test_bench_clock_sampler_starts_no_process(tmp_path, monkeypatch):
+    """The clock sampler runs inside the process that drives the GPU, so it must never
+    start another program: under rocprofv3 the profiler's preloaded library would
+    come along and the child's exec would happen from a GPU-initialised process. Every
+    way of starting a process is patched to raise; the sampler still returns the clock
+    from a sysfs-layout file (and None when the file is missing), and the steps it ran."""
+    import os
+    import subprocess
+
+    bench = _bench_module()
+    started = []
+
+    def refuse(*args, **kwargs):
+        started.append(args)
+        raise AssertionError("the clock sampler started a process")
+
+    monkeypatch.setattr(subprocess, "Popen", refuse)
+    monkeypatch.setattr(subprocess, "run", refuse)
+    for name in ("system", "fork", "posix_spawn", "posix_spawnp", "execv", "execve", "execvp", "execvpe",
+                 "spawnv", "spawnve", "popen"):
+        if hasattr(os, name):
+            monkeypatch.setattr(os, name, refuse)
+
+    sysfs = tmp_path / "pp_dpm_sclk"
+    sysfs.write_text("0: 500Mhz\n1: 2105Mhz *\n2: 2400Mhz\n")
+    steps = []
+    mhz, ran = bench.sample_sclk_mhz(lambda: steps.append(1), lambda: None, files=[sysfs], reads=3)
+    assert mhz == 2105.0
+    assert ran == len(steps) and ran > 0
+    mhz, _ = bench.sample_sclk_mhz(lambda: None, lambda: None, files=[tmp_path / "missing"], reads=3)
+    assert mhz is None
+    mhz, _ = bench.sample_sclk_mhz(lambda: None, lambda: None, files=[], reads=3)
+    assert mhz is None
+    assert started == []

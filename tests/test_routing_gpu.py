@@ -85,6 +85,8 @@ def _host_importance(q, k, M, N, d, tr, tk, fraction):
     (2, 1000, 5000, 16, 16, 32, 0.3, "normal"),  # 9891 tiles: a ragged last wave of register keys
     (1, 1000, 5000, 16, 16, 32, 0.75, "zeros"),  # selected key 0, tied with the ragged padding
     (1, 4096, 8192, 16, 16, 32, 0.45, "ties"),  # 65536 tiles: keys recomputed each pass
+    # tiles_q + tiles_k = 15360 + 1024 = 16384, the select's LDS limit (64 KiB of factors)
+    (1, 16 * 15360, 32 * 1024, 16, 16, 32, 0.25, "outlier"),
 ])
 def test_importance_matches_host_router(tm, cuda, heads, M, N, d, tr, tk, fraction, pattern):
     import torch

@@ -2,7 +2,8 @@
 against the workspace entry point it mirrors (tilemix_tiles_importance),
 through the C ABI: two calls in a row on the same library scratch, the second
 with a smaller problem, each equal byte for byte to the workspace call on the
-same inputs; plus the size limit and argument checks."""
+same inputs. Its size limit and argument checks run without a GPU in
+tests/test_capi_cpu.py::test_mask_producer_validation_codes."""
 from __future__ import annotations
 
 import numpy as np

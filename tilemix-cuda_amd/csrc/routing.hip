@@ -554,9 +554,19 @@ hipError_t scratch_address(float** out) {
     if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> guard(lock);
     if (!address[device]) {
+        // The first call on a device may come while the caller's stream is
+        // being captured into a graph. The lookup enqueues no work, so this
+        // thread's capture mode is relaxed around it (a global-mode capture
+        // would otherwise reject the runtime call and invalidate the graph),
+        // then restored.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        status = hipThreadExchangeStreamCaptureMode(&mode);
+        if (status != hipSuccess) return status;
         void* ptr = nullptr;
         status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        const hipError_t restored = hipThreadExchangeStreamCaptureMode(&mode);
         if (status != hipSuccess) return status;
+        if (restored != hipSuccess) return restored;
         address[device] = static_cast<float*>(ptr);
     }
     *out = address[device];
