@@ -1,8 +1,9 @@
 """Build the native test programs under tests/native/_build/.
 
-* tilemix_test restates src/tests/tilemix_test.cu against the HIP library's
-  C++ API (include/attention_fused.h) and links the C oracle as its checker;
-  build the library first (tilemix-cuda_amd/build.py).
+* tilemix_native runs the API validation table, the closed forms and every
+  dense and routed GPU case through the HIP library's C++ API
+  (include/attention_fused.h), with the C oracle linked as its checker; build
+  the library first (tilemix-cuda_amd/build.py).
 * quant_division_check runs the quantizer's division-free quotient against
   IEEE division for every fp16 (block maximum, value) pair, compiled with the
   library's own device flags.
@@ -20,7 +21,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parent.parent
 OUT = HERE / "_build"
-EXE = OUT / "tilemix_test"
+EXE = OUT / "tilemix_native"
 DIVISION_CHECK = OUT / "quant_division_check"
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
@@ -36,9 +37,9 @@ def build() -> Path:
     oracle_obj = OUT / "tilemix_oracle.o"
     _run(["gcc", "-O2", "-std=c99", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
           "-c", str(ROOT / "oracle" / "tilemix_oracle.c"), "-o", str(oracle_obj)])
-    test_obj = OUT / "tilemix_test.o"
+    test_obj = OUT / "tilemix_native.o"
     _run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", f"-I{ROOT / 'include'}", f"-I{ROOT / 'oracle'}",
-          "-Wno-unused-command-line-argument", "-c", str(HERE / "tilemix_test.cpp"), "-o", str(test_obj)])
+          "-Wno-unused-command-line-argument", "-c", str(HERE / "tilemix_native.cpp"), "-o", str(test_obj)])
     tmp = EXE.with_suffix(".tmp")
     _run([HIPCC, "--offload-arch=gfx950", str(test_obj), str(oracle_obj), "-fopenmp",
           f"-L{ROOT / 'tilemix-cuda_amd'}", "-ltilemix_hip", "-Wl,-rpath,$ORIGIN/../../../tilemix-cuda_amd",

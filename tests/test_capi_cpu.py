@@ -1,8 +1,9 @@
 """The C-ABI library without a GPU: it loads, exports exactly what
 include/tilemix_capi.h declares, answers the sizing helpers, and returns the
 reference's validation codes before any HIP runtime call
-(src/tests/tilemix_test.cu:157-234 is the list of cases). Also runs the native
-test driver's CPU mode and checks that the product never reaches the oracle.
+(src/tests/tilemix_test.cu:157-234 is the list of cases), and the product never
+reaches the oracle. The native program's CPU mode is run by
+tests/test_native_export.py.
 """
 from __future__ import annotations
 
@@ -230,12 +231,3 @@ def test_product_never_uses_the_oracle():
     assert not offenders, offenders
     deps = subprocess.run(["ldd", str(api.library_path())], capture_output=True, text=True).stdout
     assert "oracle" not in deps
-
-
-def test_native_driver_cpu_mode():
-    exe = ROOT / "tests" / "native" / "_build" / "tilemix_test"
-    assert exe.exists(), "build with `python tests/native/build.py` (or __graft_entry__.build())"
-    out = subprocess.run([str(exe), "--cpu-only"], capture_output=True, text=True, timeout=300)
-    assert out.returncode == 0, out.stderr
-    assert "PASS TileMix API validation and sizing helpers (no HIP runtime call)" in out.stdout
-    assert out.stdout.count("PASS") >= 6
