@@ -35,7 +35,7 @@
 //    one each: the next tile's K, K8 and V are all fetched after the tile's
 //    second barrier, while softmax and P.V run, so no tile load is issued
 //    among the score MFMAs; two barriers per tile. At d = 128, 56 KiB of tile
-//    buffers plus 18 KiB of quantized Q rows let two workgroups share a CU.
+//    buffers per workgroup.
 //  * Each SIMD runs one wave of each of the CU's two workgroups. A tile is an
 //    MFMA phase (P.V, barrier, next scores) and a VALU phase (softmax). A
 //    wave's issue priority is low in the first half of each phase and high
@@ -47,7 +47,9 @@
 //    masks; a wave whose cells mix routes computes both score kinds and
 //    selects per lane.
 //  * The optional in-kernel Q quantization reproduces quantize_tilemix_qk's
-//    bytes exactly: the workgroup's 128 rows are exactly one Q block.
+//    bytes exactly: the workgroup's 128 rows are exactly one Q block. The
+//    bytes reach the INT8 operand layout through a lane swap between the
+//    two halves of the wave, not through LDS.
 
 #include "attention_common.h"
 #include "tilemix_capi.h"
@@ -55,6 +57,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 namespace tilemix {
 namespace {
@@ -96,8 +99,6 @@ struct Layout {
     static constexpr int kKPerWave = (kKLoads + kWavesPerGroup - 1) / kWavesPerGroup;
     static constexpr int kVPerWave = (kVLoads + kWavesPerGroup - 1) / kWavesPerGroup;
     static constexpr int kK8PerWave = (kK8Loads + kWavesPerGroup - 1) / kWavesPerGroup;
-    static constexpr int kQ8Stride = kDP8 + 16;    // the workgroup's quantized Q rows
-    static constexpr int kQ8Bytes = kRowsPerGroup * kQ8Stride;
     // K, V buffer 0, K8, V buffer 1.
     static constexpr int kV1Offset = kVBytes + kK8Bytes;  // V buffer 1 - V buffer 0
     static constexpr int kSmemBytes = kKBytes + kVBytes + kK8Bytes + kVBytes;
@@ -261,7 +262,10 @@ __device__ __forceinline__ void load_slots(int4v rsrc, unsigned first, const int
     load_slots_from<0, kSlots>(rsrc, first, voffset, soffset);
 }
 
-template <int DC, bool kVector, bool kPrecise, bool kDots>
+// kSplit: the workgroup covers one range of key tiles of its 128-row block
+// and writes that range's partial row state (AttnParams::splits); only the
+// per-head entry point launches it.
+template <int DC, bool kVector, bool kPrecise, bool kDots, bool kSplit>
 __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kernel(const AttnParams p) {
     using L = Layout<DC>;
     constexpr int kDP = L::kDP;
@@ -269,8 +273,6 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     constexpr int kQC = kDP / 16;         // 16-feature Q / K chunks (fp16 MFMA k-steps)
     constexpr int kQ8C = L::kDP8 / 32;    // 32-feature Q8 / K8 chunks (int8 MFMA k-steps)
     __shared__ __attribute__((aligned(16))) unsigned char smem[L::kSmemBytes];
-    // Quantized Q rows (B operand of the INT8 MFMA), read on INT8 tiles only.
-    __shared__ __attribute__((aligned(16))) unsigned char lds_q8[L::kQ8Bytes];
     __shared__ unsigned group_bits[kWavesPerGroup];
     // Landing area of the spare DMA slots (written with zeros, never read).
     __shared__ __attribute__((aligned(16))) unsigned char lds_spare[1024];
@@ -290,7 +292,12 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     const int h = lane >> 5;  // which half of each 32-key / 16-feature block the lane holds
 
     int head32, qblock;
-    map_block(blockIdx.x, p.heads, p.q_blocks, p.causal != 0, head32, qblock);
+    int item = blockIdx.x, split = 0;
+    if constexpr (kSplit) {
+        item = blockIdx.x / p.splits;
+        split = blockIdx.x - item * p.splits;
+    }
+    map_block(item, p.heads, p.q_blocks, p.causal != 0, head32, qblock);
     const std::int64_t head = head32;
     const int q0 = qblock * kRowsPerGroup;
     const int qw = q0 + wave * kRowsPerWave;
@@ -325,6 +332,10 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         }
     }
 
+    // The wave's quantized Q rows (B operand of the INT8 MFMA), kept in
+    // registers: lane (q, h) holds features 32m + 16h .. 32m + 16h + 15 of
+    // its row for chunk m.
+    int4v q8f[kQ8C];
     float q_scale = 0.0f;
     if (p.int8_operands) {
         if (p.fuse_q_quant) {
@@ -369,11 +380,12 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             if (tid == 0 && p.q_scales_out)
                 p.q_scales_out[head * p.q_blocks + qblock] = __builtin_bit_cast(std::uint16_t, stored);
             {
-                const int local = wave * kRowsPerWave + q;
-                const int row = q0 + local;
+                const int row = qw + q;
+                // Bytes of fp16 chunk c (features 16c + 8h .. + 7 of the row).
+                uint2v packed[L::kDP8 / 16];
 #pragma unroll
                 for (int c = 0; c < L::kDP8 / 16; ++c) {
-                    uint2v packed{0u, 0u};
+                    packed[c] = uint2v{0u, 0u};
                     if (c < kQC && scale > 0.0f) {
                         const uint4v words = __builtin_bit_cast(uint4v, qf[c < kQC ? c : 0]);
                         int v[8];
@@ -382,28 +394,50 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                             v[2 * w] = quantize_half<0>(words[w], scale, recip);
                             v[2 * w + 1] = quantize_half<1>(words[w], scale, recip);
                         }
-                        packed[0] = pack_bytes(v[0], v[1], v[2], v[3]);
-                        packed[1] = pack_bytes(v[4], v[5], v[6], v[7]);
+                        packed[c][0] = pack_bytes(v[0], v[1], v[2], v[3]);
+                        packed[c][1] = pack_bytes(v[4], v[5], v[6], v[7]);
                     }
                     const int feature = 16 * c + 8 * h;
-                    *reinterpret_cast<uint2v*>(lds_q8 + local * L::kQ8Stride + feature) = packed;
                     if (p.q8_out && row < M && feature < d) {
                         std::int8_t* dst = p.q8_out + head * static_cast<std::int64_t>(M) * d +
                                            static_cast<std::int64_t>(row) * d + feature;
                         if constexpr (kVector) {
-                            *reinterpret_cast<uint2v*>(dst) = packed;
+                            *reinterpret_cast<uint2v*>(dst) = packed[c];
                         } else {
                             for (int e = 0; e < 8 && feature + e < d; ++e)
-                                dst[e] = static_cast<std::int8_t>(packed[e / 4] >> (8 * (e % 4)));
+                                dst[e] = static_cast<std::int8_t>(packed[c][e / 4] >> (8 * (e % 4)));
                         }
                     }
                 }
+                // INT8 chunk m = fp16 chunks 2m (features 32m .. 32m + 15)
+                // and 2m + 1 (32m + 16 .. 32m + 31). Lanes h = 0 keep their
+                // bytes of chunk 2m and take lane (q, 1)'s; lanes h = 1 keep
+                // their bytes of chunk 2m + 1 and take lane (q, 0)'s: one
+                // v_permlane32_swap per dword.
+#pragma unroll
+                for (int m = 0; m < kQ8C; ++m) {
+                    const uint2v keep = h ? packed[2 * m + 1] : packed[2 * m];
+                    const uint2v send = h ? packed[2 * m] : packed[2 * m + 1];
+                    std::uint32_t got[2];
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        const std::uint32_t word = send[k];  // copied out before the bit cast, see above
+                        float a = __builtin_bit_cast(float, word), b = a;
+                        permlane32_swap(a, b);  // a: lane (q, 0)'s dword, b: lane (q, 1)'s
+                        got[k] = __builtin_bit_cast(std::uint32_t, h ? a : b);
+                    }
+                    q8f[m] = h ? int4v{static_cast<int>(got[0]), static_cast<int>(got[1]), static_cast<int>(keep[0]),
+                                       static_cast<int>(keep[1])}
+                               : int4v{static_cast<int>(keep[0]), static_cast<int>(keep[1]), static_cast<int>(got[0]),
+                                       static_cast<int>(got[1])};
+                }
             }
         } else {
+            // Q8 rows already come in the operand layout: 16 bytes per lane
+            // and chunk, read straight into q8f.
             q_scale = half_bits_to_float(p.q_scales[head * p.q_blocks + qblock]);
             const std::int8_t* Q8h = p.Q8 + head * static_cast<std::int64_t>(M) * d;
-            const int local = wave * kRowsPerWave + q;
-            const int row = q0 + local;
+            const int row = qw + q;
 #pragma unroll
             for (int m = 0; m < kQ8C; ++m) {
                 const int feature = 32 * m + 16 * h;
@@ -421,10 +455,9 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                             : 0;
                     chunk = __builtin_bit_cast(int4v, bytes);
                 }
-                *reinterpret_cast<int4v*>(lds_q8 + local * L::kQ8Stride + feature) = chunk;
+                q8f[m] = chunk;
             }
         }
-        __syncthreads();  // lds_q8 complete
     }
 
     // ------------------------------------------------------ routing masks
@@ -585,13 +618,6 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         __syncthreads();
     };
 
-    // The wave's quantized Q rows (INT8 operand), kept in registers.
-    int4v q8f[kQ8C];
-    if (p.int8_operands) {
-#pragma unroll
-        for (int m = 0; m < kQ8C; ++m)
-            q8f[m] = *reinterpret_cast<const int4v*>(lds_q8 + (wave * kRowsPerWave + q) * L::kQ8Stride + 32 * m + 16 * h);
-    }
     // Per-lane LDS offsets of the K fragment (feature chunk dc, key block 0)
     // and V^T fragment (feature block fb, key step 0) reads; key blocks and
     // steps add whole rows (multiples of 16, which keep the chunk rotation).
@@ -619,6 +645,9 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     const int key_tiles64 = (N - 1) / kTileKeys + 1;
     int tiles = key_tiles64;
     if (p.causal) tiles = min(tiles, (q0 + kRowsPerGroup - 1) / kTileKeys + 1);
+    // A split workgroup covers its own range of key tiles.
+    const int tile_begin = kSplit ? split * p.split_tiles : 0;
+    if constexpr (kSplit) tiles = min(tiles, tile_begin + p.split_tiles);
     const std::int64_t trace_base = head * static_cast<std::int64_t>(p.q_tiles16) * p.key_tiles32;
     auto write_trace = [&](int j, std::uint32_t int8_mask, std::uint32_t skip_mask) {
         if (wave == 0 && lane < 16) {
@@ -648,7 +677,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     // (K, K8, and V into the other buffer) are issued after the tile's second
     // barrier: by then every wave has finished its scores (the K and K8
     // buffers are free) and the previous tile's P.V (its V buffer is free).
-    int j = next_tile(0);
+    int j = next_tile(tile_begin);
     int v_buffer = 0;
     if (j < tiles) {
         issue_k(j, needs16(cur_int8, cur_skip), cur_int8 != 0);
@@ -845,7 +874,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     }
 
     // Routing trace of tiles a causal workgroup never visits.
-    if (kDots && p.trace && tiles < key_tiles64) {
+    if (kDots && !kSplit && p.trace && tiles < key_tiles64) {
         for (int j = tiles; j < key_tiles64; ++j) {
             std::uint32_t int8_mask = 0, skip_mask = 0;
             tile_masks(j, int8_mask, skip_mask);
@@ -854,7 +883,29 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     }
 
     // ---------------------------------------------------------- epilogue
-    {
+    if constexpr (kSplit) {
+        // This split's unnormalised rows and their (m, l), for the combine.
+        float a = st.lsum, b = st.lsum;
+        permlane32_swap(a, b);
+        const int row = qw + q;
+        if (row < M) {
+            unsigned char* const part = reinterpret_cast<unsigned char*>(p.part_o + static_cast<std::int64_t>(split) * M * d);
+            const std::int64_t row_offset = static_cast<std::int64_t>(row) * d;
+#pragma unroll
+            for (int fb = 0; fb < kOB; ++fb)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int feature = (r4 < 2 ? 0 : kDP / 2 - 16) + 16 * fb + 8 * r4 + 4 * h;
+                    const float4v value{st.o[fb][4 * r4], st.o[fb][4 * r4 + 1], st.o[fb][4 * r4 + 2], st.o[fb][4 * r4 + 3]};
+                    store_output(part, TILEMIX_DTYPE_F32, row_offset + feature, value, d - feature, kVector);
+                }
+            if (h == 0) {
+                float* const ml = p.part_ml + 2 * (static_cast<std::int64_t>(split) * M + row);
+                ml[0] = st.m;
+                ml[1] = a + b;
+            }
+        }
+    } else {
         float a = st.lsum, b = st.lsum;
         permlane32_swap(a, b);  // the row's other half, held by lane ^ 32
         const float l = a + b;
@@ -876,18 +927,78 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     }
 }
 
-template <int DC, bool kVector, bool kPrecise, bool kDots>
+// O of a key-range split launch: per row, m = max over the splits of m_s,
+// O = sum_s 2^(m_s - m) O_s / sum_s 2^(m_s - m) l_s (log2-domain row states;
+// splits whose rows saw no key have m_s = -inf and weigh nothing). One
+// thread per row and 4 features, splits summed in order.
+// Splits are taken kBatch at a time with all of a batch's loads issued
+// before any use.
+template <bool kVector>
+__global__ __launch_bounds__(256) void split_combine_kernel(const float* part_o, const float* part_ml, int splits,
+                                                           int M, int d, float* O, std::int64_t o_row) {
+    constexpr int kBatch = 8;
+    const int groups = (d + 3) / 4;
+    const std::int64_t index = static_cast<std::int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (index >= static_cast<std::int64_t>(M) * groups) return;
+    const int row = static_cast<int>(index / groups);
+    const int f0 = 4 * static_cast<int>(index - static_cast<std::int64_t>(row) * groups);
+    const float2v* const ml = reinterpret_cast<const float2v*>(part_ml);
+    float m = -INFINITY;
+    for (int s = 0; s < splits; ++s) m = fmaxf(m, ml[static_cast<std::int64_t>(s) * M + row][0]);
+    float l = 0.0f;
+    float4v acc{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < splits; s0 += kBatch) {
+        float2v state[kBatch];
+        float4v value[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const std::int64_t r = static_cast<std::int64_t>(s0 + b < splits ? s0 + b : s0) * M + row;
+            state[b] = ml[r];
+            const float* src = part_o + r * d + f0;
+            if constexpr (kVector) {
+                value[b] = *reinterpret_cast<const float4v*>(src);
+            } else {
+                for (int e = 0; e < 4; ++e) value[b][e] = f0 + e < d ? src[e] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const float w = (s0 + b >= splits || state[b][0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(state[b][0] - m);
+            l += w * state[b][1];
+            acc += w * value[b];
+        }
+    }
+    const float inverse = l > 0.0f ? 1.0f / l : 0.0f;
+    float* dst = O + static_cast<std::int64_t>(row) * o_row + f0;
+    if constexpr (kVector) {
+        *reinterpret_cast<float4v*>(dst) = acc * inverse;
+    } else {
+        for (int e = 0; e < 4 && f0 + e < d; ++e) dst[e] = acc[e] * inverse;
+    }
+}
+
+template <int DC, bool kVector, bool kPrecise, bool kDots, bool kSplit>
 hipError_t launch_variant(const AttnParams& p, hipStream_t stream) {
-    const unsigned blocks = static_cast<unsigned>(p.q_blocks) * static_cast<unsigned>(p.heads);
-    attention_kernel<DC, kVector, kPrecise, kDots><<<blocks, kThreadsPerGroup, 0, stream>>>(p);
+    const unsigned blocks = static_cast<unsigned>(p.q_blocks) * static_cast<unsigned>(p.heads) *
+                            static_cast<unsigned>(kSplit ? p.splits : 1);
+    attention_kernel<DC, kVector, kPrecise, kDots, kSplit><<<blocks, kThreadsPerGroup, 0, stream>>>(p);
     return hipGetLastError();
 }
 
+// Split launches exist for the per-head entry point only, whose P.V is
+// always the precise one.
 template <int DC, bool kVector>
 hipError_t launch_vp(const AttnParams& p, bool precise, bool dots, hipStream_t stream) {
+    if (p.splits > 1) {
+        if (!precise) return hipErrorInvalidValue;
+        return dots ? launch_variant<DC, kVector, true, true, true>(p, stream)
+                    : launch_variant<DC, kVector, true, false, true>(p, stream);
+    }
     if (precise)
-        return dots ? launch_variant<DC, kVector, true, true>(p, stream) : launch_variant<DC, kVector, true, false>(p, stream);
-    return dots ? launch_variant<DC, kVector, false, true>(p, stream) : launch_variant<DC, kVector, false, false>(p, stream);
+        return dots ? launch_variant<DC, kVector, true, true, false>(p, stream)
+                    : launch_variant<DC, kVector, true, false, false>(p, stream);
+    return dots ? launch_variant<DC, kVector, false, true, false>(p, stream)
+                : launch_variant<DC, kVector, false, false, false>(p, stream);
 }
 
 template <int DC>
@@ -912,23 +1023,35 @@ std::size_t word_count(int M, int N, int group) {
 }
 
 // gfx950 check, cached per device (the reference queries device properties
-// on every call, src/tilemix.cu:254-260).
-hipError_t check_device() {
-    constexpr int kMaxDevices = 64;
+// on every call, src/tilemix.cu:254-260), with the device's compute-unit
+// count (0 when the device is not cached).
+constexpr int kMaxDevices = 64;
+
+hipError_t check_device(int* compute_units = nullptr) {
     static std::atomic<int> verdict[kMaxDevices];  // 0 unknown, 1 supported, 2 unsupported
+    static std::atomic<int> units[kMaxDevices];
     int device = 0;
     hipError_t status = hipGetDevice(&device);
     if (status != hipSuccess) return status;
-    if (device >= 0 && device < kMaxDevices) {
+    const bool cached = device >= 0 && device < kMaxDevices;
+    if (compute_units) *compute_units = 0;
+    if (cached) {
         const int known = verdict[device].load(std::memory_order_relaxed);
-        if (known == 1) return hipSuccess;
         if (known == 2) return hipErrorNotSupported;
+        if (known == 1) {
+            if (compute_units) *compute_units = units[device].load(std::memory_order_relaxed);
+            return hipSuccess;
+        }
     }
     hipDeviceProp_t properties{};
     status = hipGetDeviceProperties(&properties, device);
     if (status != hipSuccess) return status;
     const bool supported = std::strncmp(properties.gcnArchName, "gfx950", 6) == 0;
-    if (device >= 0 && device < kMaxDevices) verdict[device].store(supported ? 1 : 2, std::memory_order_relaxed);
+    if (cached) {
+        units[device].store(properties.multiProcessorCount, std::memory_order_relaxed);
+        verdict[device].store(supported ? 1 : 2, std::memory_order_relaxed);
+        if (compute_units) *compute_units = properties.multiProcessorCount;
+    }
     return supported ? hipSuccess : hipErrorNotSupported;
 }
 
@@ -957,6 +1080,114 @@ hipError_t launch_attention(const AttnParams& p, bool precise, hipStream_t strea
         case 3: return launch_dc<3>(p, vector, precise, stream);
         default: return launch_dc<4>(p, vector, precise, stream);
     }
+}
+
+}  // namespace
+}  // namespace tilemix
+
+// Workspace of the per-head entry point's key-range split (partial O rows and
+// row states of every split, [splits][M][d] + [splits][M][2] fp32). One copy
+// per GPU, held until the process ends; the library allocates nothing.
+// Split calls on a device are ordered through one event (each waits for the
+// previous split call's combine, whatever its stream), so concurrent streams
+// never share it at once; calls made while their stream is being captured
+// into a graph take the plain launch instead.
+static constexpr std::size_t kSplitScratchFloats = std::size_t{8} << 20;  // 32 MiB
+static __device__ __align__(256) float split_scratch[kSplitScratchFloats];
+
+namespace tilemix {
+namespace {
+
+// A split covers at least this many key tiles, so that its prologue (the
+// Q block's load and staging) stays small against its loop.
+#ifndef TILEMIX_MIN_SPLIT_TILES
+#define TILEMIX_MIN_SPLIT_TILES 4
+#endif
+constexpr int kMinSplitTiles = TILEMIX_MIN_SPLIT_TILES;
+
+struct SplitDevice {
+    float* scratch = nullptr;
+    hipEvent_t done = nullptr;
+    bool recorded = false;
+};
+
+std::mutex& split_lock() {
+    static std::mutex lock;
+    return lock;
+}
+
+SplitDevice* split_devices() {
+    static SplitDevice devices[kMaxDevices];
+    return devices;
+}
+
+// Key-range splits for a single-head, non-causal launch that would fill less
+// than half of the device's workgroup slots: as many as bring it to one
+// wave of workgroups, each covering at least kMinSplitTiles key tiles and
+// all fitting in the workspace (1 = no split).
+int choose_splits(const AttnParams& p, int compute_units) {
+    if (compute_units <= 0 || p.heads != 1 || p.causal) return 1;
+    const int resident = compute_units * kGroupsPerCU;
+    if (2 * p.q_blocks > resident) return 1;
+    const int tiles = (p.N - 1) / kTileKeys + 1;
+    int splits = std::min(resident / p.q_blocks, tiles / kMinSplitTiles);
+    while (splits > 1 && static_cast<std::size_t>(splits) * p.M * (p.d + 2) > kSplitScratchFloats) --splits;
+    return splits > 1 ? splits : 1;
+}
+
+// launch_attention, with the key range split over several workgroups per
+// 128-row block when choose_splits says so: the attention kernel writes each
+// split's partial rows to the workspace, split_combine_kernel merges them
+// into O, both on `stream`.
+hipError_t launch_attention_split(AttnParams p, bool precise, hipStream_t stream) {
+    int units = 0;
+    hipError_t status = check_device(&units);
+    if (status != hipSuccess) return status;
+    int splits = choose_splits(p, units);
+    if (splits > 1) {
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone) splits = 1;
+    }
+    int device = 0;
+    if (splits > 1 && (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices)) splits = 1;
+    if (splits <= 1) return launch_attention(p, precise, stream);
+
+    std::lock_guard<std::mutex> guard(split_lock());
+    SplitDevice& state = split_devices()[device];
+    if (!state.scratch) {
+        void* address = nullptr;
+        status = hipGetSymbolAddress(&address, HIP_SYMBOL(split_scratch));
+        if (status != hipSuccess) return status;
+        state.scratch = static_cast<float*>(address);
+    }
+    if (!state.done) {
+        status = hipEventCreateWithFlags(&state.done, hipEventDisableTiming);
+        if (status != hipSuccess) return status;
+    }
+    if (state.recorded) {
+        status = hipStreamWaitEvent(stream, state.done, 0);
+        if (status != hipSuccess) return status;
+    }
+    const int tiles = (p.N - 1) / kTileKeys + 1;
+    p.split_tiles = (tiles + splits - 1) / splits;
+    p.splits = (tiles + p.split_tiles - 1) / p.split_tiles;
+    p.part_o = state.scratch;
+    p.part_ml = state.scratch + static_cast<std::size_t>(p.splits) * p.M * p.d;
+    status = launch_attention(p, precise, stream);
+    if (status != hipSuccess) return status;
+    float* const O = static_cast<float*>(p.O);
+    const std::int64_t threads = static_cast<std::int64_t>(p.M) * ((p.d + 3) / 4);
+    const unsigned blocks = static_cast<unsigned>((threads + 255) / 256);
+    if (p.d % 4 == 0 && aligned(O, 16) && p.o_row % 4 == 0)
+        split_combine_kernel<true><<<blocks, 256, 0, stream>>>(p.part_o, p.part_ml, p.splits, p.M, p.d, O, p.o_row);
+    else
+        split_combine_kernel<false><<<blocks, 256, 0, stream>>>(p.part_o, p.part_ml, p.splits, p.M, p.d, O, p.o_row);
+    status = hipGetLastError();
+    if (status != hipSuccess) return status;
+    status = hipEventRecord(state.done, stream);
+    if (status != hipSuccess) return status;
+    state.recorded = true;
+    return hipSuccess;
 }
 
 AttnParams base_params(const std::uint16_t* Q, const std::uint16_t* K, const std::uint16_t* V, float* O,
@@ -1022,7 +1253,8 @@ extern "C" int tilemix_attention(const std::uint16_t* Q, const std::uint16_t* K,
     p.k_scales = k_scales;
     // The per-head API keeps the reference's fp32-level accuracy (its own test
     // suite checks 1e-5 + 1e-4|x| against fp64), so P.V runs in split precision.
-    return launch_attention(p, /*precise=*/true, static_cast<hipStream_t>(stream));
+    // A head too small to fill the device has its key range split.
+    return launch_attention_split(p, /*precise=*/true, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int tilemix_attention_batched(const TileMixBatchedArgs* args, void* stream) {

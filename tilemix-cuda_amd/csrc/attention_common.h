@@ -68,6 +68,14 @@ struct AttnParams {
     int o_dtype;  // TILEMIX_DTYPE_F32 / _F16 / _BF16
     float score_log2;  // score_scale * log2(e)
     float score_scale;
+    // Key-range split (splits > 1): workgroup b takes tiles [s * split_tiles,
+    // (s + 1) * split_tiles) of item b / splits (s = b % splits) and writes
+    // its unnormalised O rows to part_o ([splits][M][d] fp32) and its row
+    // maximum and sum (log2 domain) to part_ml ([splits][M][2]) instead of O.
+    int splits;
+    int split_tiles;
+    float* part_o;
+    float* part_ml;
 };
 
 __device__ __forceinline__ half8 concat(half4 a, half4 b) {
