@@ -460,12 +460,20 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         }
     }
 
+    // Key tiles are visited first to last, or last to first in a reversed
+    // round (AttnParams::reverse_slots; the online softmax takes the tiles in
+    // any order).
+    const int step = (!kSplit && reversed_round(blockIdx.x, p.reverse_slots)) ? -1 : 1;
+
     // ------------------------------------------------------ routing masks
     // One pass decodes four tiles: lane 16t + c decodes cell c (row c / 2,
     // key half c % 2) of tile jb + t from the route / skip word it keeps for
-    // its query tile; the word is reloaded only when the tile's group crosses
-    // into the next 64-group block. The two 64-bit ballots hold the four
-    // tiles' wave-uniform masks, bit 16t + 2r + h <-> tile jb + t, cell (r, h).
+    // its query tile; the word is reloaded only when the tile's group moves
+    // to another 64-group block. The two 64-bit ballots hold the four tiles'
+    // wave-uniform masks, bit 16t + 2r + h <-> tile jb + t, cell (r, h). The
+    // pass starts at the tile asked for (jb = j) when the walk goes forward,
+    // and ends at it (jb = j - 3) when it goes backward; tiles before the
+    // first read as skipped.
     const int qt0 = q0 / 16;
     const int my_qt = qt0 + ((lane & 15) >> 1);
     const bool my_row_valid = my_qt < p.q_tiles16;
@@ -476,11 +484,11 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     std::uint64_t batch_int8 = 0, batch_skip = 0;
     int batch_first = -4;
     auto tile_masks = [&](int j, std::uint32_t& int8_mask, std::uint32_t& skip_mask) {
-        if (j >= batch_first + 4) {
-            batch_first = j;
-            const int kt = 2 * (j + (lane >> 4)) + (lane & 1);
+        if (static_cast<unsigned>(j - batch_first) >= 4u) {
+            batch_first = step < 0 ? j - 3 : j;
+            const int kt = 2 * (batch_first + (lane >> 4)) + (lane & 1);
             bool skip = true, int8 = false;
-            if (my_row_valid && kt < p.key_tiles32) {
+            if (my_row_valid && kt >= 0 && kt < p.key_tiles32) {
                 const unsigned group = p.group_shift >= 0 ? static_cast<unsigned>(kt) >> p.group_shift
                                                           : static_cast<unsigned>(kt) / static_cast<unsigned>(p.key_tiles_per_group);
                 const std::int64_t block = group >> 6;
@@ -647,7 +655,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     if (p.causal) tiles = min(tiles, (q0 + kRowsPerGroup - 1) / kTileKeys + 1);
     // A split workgroup covers its own range of key tiles.
     const int tile_begin = kSplit ? split * p.split_tiles : 0;
-    if constexpr (kSplit) tiles = min(tiles, tile_begin + p.split_tiles);
+    if constexpr (kSplit) tiles = max(tile_begin, min(tiles, tile_begin + p.split_tiles));
     const std::int64_t trace_base = head * static_cast<std::int64_t>(p.q_tiles16) * p.key_tiles32;
     auto write_trace = [&](int j, std::uint32_t int8_mask, std::uint32_t skip_mask) {
         if (wave == 0 && lane < 16) {
@@ -661,12 +669,19 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         return ((~int8_mask & ~skip_mask) & 0xffffu) != 0;
     };
 
+    // The loop visits tiles tile_begin .. tiles - 1 in the order of `step`;
+    // in_walk(j) says whether j is still inside that range. The walk starts
+    // at one end (tiles >= tile_begin: N >= 1, and a split's range is
+    // clamped) and moves by one tile, so it reaches tile_end exactly.
+    const int tile_end = step > 0 ? tiles : tile_begin - 1;
+    auto in_walk = [&](int j) { return j != tile_end; };
     // Tiles whose 16 cells are all skipped are stepped over: next_tile(j)
-    // returns the first tile >= j with a visible cell (or `tiles`) and its
-    // masks, writing the routing trace of the tiles it passes.
+    // returns the first tile from j on (in the walk's order) with a visible
+    // cell, or the first tile past the range, with that tile's masks,
+    // writing the routing trace of the tiles it passes.
     std::uint32_t cur_int8 = 0, cur_skip = 0;
     auto next_tile = [&](int j) {
-        for (; j < tiles; ++j) {
+        for (; in_walk(j); j += step) {
             tile_masks(j, cur_int8, cur_skip);
             if (kDots && p.trace) write_trace(j, cur_int8, cur_skip);
             if (cur_skip != 0xffffu) break;
@@ -677,9 +692,9 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     // (K, K8, and V into the other buffer) are issued after the tile's second
     // barrier: by then every wave has finished its scores (the K and K8
     // buffers are free) and the previous tile's P.V (its V buffer is free).
-    int j = next_tile(tile_begin);
+    int j = next_tile(step > 0 ? tile_begin : tiles - 1);
     int v_buffer = 0;
-    if (j < tiles) {
+    if (in_walk(j)) {
         issue_k(j, needs16(cur_int8, cur_skip), cur_int8 != 0);
         issue_v(j, v_buffer);
     }
@@ -688,7 +703,7 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
     // (rows above a causal diagonal, or all its cells skipped) takes part in
     // the tile's loads and barriers only: its probabilities would all be 0,
     // so the softmax and P.V would leave m, l and O unchanged.
-    while (j < tiles) {
+    while (in_walk(j)) {
         const int k0 = j * kTileKeys;
         const std::uint32_t int8_mask = cur_int8, skip_mask = cur_skip;
         tile_barrier();  // K_j, V_j landed; every wave finished P.V of the previous tile
@@ -834,8 +849,8 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 
         tile_barrier();  // every wave finished reading K_j (and P.V of the previous tile)
         set_priority<0>();  // first half of the VALU phase
-        const int j_next = next_tile(j + 1);
-        if (j_next < tiles) {
+        const int j_next = next_tile(j + step);
+        if (in_walk(j_next)) {
             issue_k(j_next, needs16(cur_int8, cur_skip), cur_int8 != 0);
             issue_v(j_next, v_buffer ^ 1);
         }
@@ -1055,10 +1070,17 @@ hipError_t check_device(int* compute_units = nullptr) {
     return supported ? hipSuccess : hipErrorNotSupported;
 }
 
-hipError_t launch_attention(const AttnParams& p, bool precise, hipStream_t stream) {
+hipError_t launch_attention(AttnParams p, bool precise, hipStream_t stream) {
     if (static_cast<long long>(p.q_blocks) * p.heads > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-    hipError_t status = check_device();
+    int units = 0;
+    hipError_t status = check_device(&units);
     if (status != hipSuccess) return status;
+    // Non-causal heads in the per-XCD head-major order whose query blocks
+    // outnumber an XCD's workgroup slots stream K / V once per round of
+    // slots; alternate rounds walk the keys in opposite directions.
+    const int xcd_slots = units / kXcds * kGroupsPerCU;
+    p.reverse_slots = (!p.causal && p.splits <= 1 && p.heads % kXcds == 0 && xcd_slots > 0 && p.q_blocks > xcd_slots)
+                          ? xcd_slots : 0;
     // The vector path moves 16-byte pieces and addresses a head's K / V with
     // 32-bit buffer offsets; other shapes take the element-wise path.
     const std::int64_t k_range = (static_cast<std::int64_t>(p.N - 1) * p.k_row + p.d) * 2;

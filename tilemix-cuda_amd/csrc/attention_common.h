@@ -76,6 +76,12 @@ struct AttnParams {
     int split_tiles;
     float* part_o;
     float* part_ml;
+    // > 0: the workgroups one XCD holds at once (its slots). A head whose
+    // query blocks span several rounds of that many workgroups streams its
+    // K / V once per round; a workgroup of an odd round walks its key tiles
+    // last to first, so it starts on the tiles the round before it left in
+    // the XCD's L2. 0: every workgroup walks first to last.
+    int reverse_slots;
 };
 
 __device__ __forceinline__ half8 concat(half4 a, half4 b) {
@@ -269,6 +275,12 @@ __device__ __forceinline__ void map_block(int linear, int heads, int groups, boo
         slot_group = linear % groups;
     }
     group = causal ? groups - 1 - slot_group : slot_group;
+}
+
+// Whether workgroup `linear` (dealt to XCD linear % kXcds) runs in an odd
+// round of `reverse_slots` workgroups on its XCD (AttnParams::reverse_slots).
+__device__ __forceinline__ bool reversed_round(int linear, int reverse_slots) {
+    return reverse_slots > 0 && ((linear / kXcds / reverse_slots) & 1) != 0;
 }
 
 }  // namespace tilemix
