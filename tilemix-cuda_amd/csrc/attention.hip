@@ -945,22 +945,22 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
 // O of a key-range split launch: per row, m = max over the splits of m_s,
 // O = sum_s 2^(m_s - m) O_s / sum_s 2^(m_s - m) l_s (log2-domain row states;
 // splits whose rows saw no key have m_s = -inf and weigh nothing). One
-// thread per row and 4 features, splits summed in order.
-// Splits are taken kBatch at a time with all of a batch's loads issued
-// before any use.
+// thread per row and 4 features, splits summed in order. Splits are taken
+// kBatch at a time, every load of a batch issued before any use (one memory
+// round trip per batch); m is the maximum over the splits seen so far, and a
+// later batch that raises it rescales the sums (up to kBatch splits: one
+// batch, m over all splits).
 template <bool kVector>
 __global__ __launch_bounds__(256) void split_combine_kernel(const float* part_o, const float* part_ml, int splits,
                                                            int M, int d, float* O, std::int64_t o_row) {
-    constexpr int kBatch = 8;
+    constexpr int kBatch = 16;
     const int groups = (d + 3) / 4;
     const std::int64_t index = static_cast<std::int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (index >= static_cast<std::int64_t>(M) * groups) return;
     const int row = static_cast<int>(index / groups);
     const int f0 = 4 * static_cast<int>(index - static_cast<std::int64_t>(row) * groups);
     const float2v* const ml = reinterpret_cast<const float2v*>(part_ml);
-    float m = -INFINITY;
-    for (int s = 0; s < splits; ++s) m = fmaxf(m, ml[static_cast<std::int64_t>(s) * M + row][0]);
-    float l = 0.0f;
+    float m = -INFINITY, l = 0.0f;
     float4v acc{0.0f, 0.0f, 0.0f, 0.0f};
     for (int s0 = 0; s0 < splits; s0 += kBatch) {
         float2v state[kBatch];
@@ -975,6 +975,17 @@ __global__ __launch_bounds__(256) void split_combine_kernel(const float* part_o,
             } else {
                 for (int e = 0; e < 4; ++e) value[b][e] = f0 + e < d ? src[e] : 0.0f;
             }
+        }
+        float m_next = m;
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+            if (s0 + b < splits) m_next = fmaxf(m_next, state[b][0]);
+        if (m_next == -INFINITY) continue;  // no split so far saw a key of this row
+        if (m_next != m) {
+            const float rescale = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_next);
+            l *= rescale;
+            acc *= rescale;
+            m = m_next;
         }
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) {
