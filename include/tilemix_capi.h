@@ -8,9 +8,10 @@
  *   - fp16 tensors are passed as `uint16_t*` holding IEEE binary16 bit
  *     patterns (the storage of `__half`);
  *   - every pointer is a device pointer owned by the caller; the library
- *     allocates nothing and keeps no state between calls (a cached
- *     per-device capability check and the fixed scratch array of
- *     tilemix_tiles_importance_noalloc aside);
+ *     allocates no device memory and keeps no state between calls besides
+ *     a cached per-device capability check, the fixed scratch array of
+ *     tilemix_tiles_importance_noalloc, and the fixed split workspace and
+ *     one ordering event per device of tilemix_attention (see there);
  *   - `stream` is a `hipStream_t` (NULL = the default stream); all work is
  *     enqueued on it and nothing synchronises;
  *   - the return value is a `hipError_t` code (0 = hipSuccess). Argument
@@ -59,6 +60,13 @@ int tilemix_quantize_qk(const uint16_t* Q, const uint16_t* K, int8_t* Q8, int8_t
  * bytes) receives the decoded bit of every cell; score_dots (optional, M*N
  * int32) receives the raw int32 dot of every INT8-routed (q, k).
  * Validation order and codes follow src/tilemix.cu:242-266.
+ * A head too small to fill the device (its 128-row blocks under half of the
+ * workgroup slots) has its key range split over several workgroups per
+ * block, whose partial rows go to a fixed 32 MiB device array inside the
+ * library (one per GPU) and are merged into O by a second kernel on
+ * `stream`. Split calls on one device are ordered through one event (each
+ * waits for the previous one's merge, on any stream); a call made while
+ * `stream` is being captured into a graph takes the unsplit launch.
  */
 int tilemix_attention(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* O,
                       int M, int N, int d, float score_scale, void* stream,
