@@ -1132,11 +1132,10 @@ namespace tilemix {
 namespace {
 
 // A split covers at least this many key tiles, so that its prologue (the
-// Q block's load and staging) stays small against its loop.
-#ifndef TILEMIX_MIN_SPLIT_TILES
-#define TILEMIX_MIN_SPLIT_TILES 4
-#endif
-constexpr int kMinSplitTiles = TILEMIX_MIN_SPLIT_TILES;
+// Q block's load) and its partial-row stores stay small against its loop
+// (measured on 64 per-head calls of 4096 x 4096 x 128: at least 4 tiles per
+// split is level with 2 and faster than 8 or 16).
+constexpr int kMinSplitTiles = 4;
 
 struct SplitDevice {
     float* scratch = nullptr;
@@ -1187,15 +1186,23 @@ hipError_t launch_attention_split(AttnParams p, bool precise, hipStream_t stream
 
     std::lock_guard<std::mutex> guard(split_lock());
     SplitDevice& state = split_devices()[device];
-    if (!state.scratch) {
-        void* address = nullptr;
-        status = hipGetSymbolAddress(&address, HIP_SYMBOL(split_scratch));
+    if (!state.scratch || !state.done) {
+        // First split call on this device: another thread may be capturing a
+        // graph in global mode, which would reject these runtime calls (they
+        // enqueue no work), so this thread's capture mode is relaxed around
+        // them and then restored.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        status = hipThreadExchangeStreamCaptureMode(&mode);
         if (status != hipSuccess) return status;
-        state.scratch = static_cast<float*>(address);
-    }
-    if (!state.done) {
-        status = hipEventCreateWithFlags(&state.done, hipEventDisableTiming);
+        if (!state.scratch) {
+            void* address = nullptr;
+            status = hipGetSymbolAddress(&address, HIP_SYMBOL(split_scratch));
+            if (status == hipSuccess) state.scratch = static_cast<float*>(address);
+        }
+        if (status == hipSuccess && !state.done) status = hipEventCreateWithFlags(&state.done, hipEventDisableTiming);
+        const hipError_t restored = hipThreadExchangeStreamCaptureMode(&mode);
         if (status != hipSuccess) return status;
+        if (restored != hipSuccess) return restored;
     }
     if (state.recorded) {
         status = hipStreamWaitEvent(stream, state.done, 0);
