@@ -926,6 +926,68 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         const float l = a + b;
         const float inverse = l > 0.0f ? 1.0f / l : 0.0f;
         const int row = qw + q;
+        // fp32 O of 128-feature rows (the variants without dot export) goes
+        // out through LDS. From registers, each store instruction writes 16
+        // bytes to each of 32 rows, i.e. 32 partial cache lines, and those
+        // lines, held in the XCD's L2 until written back, evict K / V tiles.
+        // Staged, each store writes 8 rows x 128 bytes (full cache lines)
+        // with a non-temporal hint, so O bypasses the L2. The stage buffer is
+        // the K tile buffer: every wave has passed the last tile's second
+        // barrier, so no wave reads it any more and no load targets it. Each
+        // wave stages its 32 rows in four passes of 32 features through a
+        // 4 KiB quarter of it.
+        if constexpr (kVector && !kDots && kDP == 128) {
+            if (p.o_dtype == TILEMIX_DTYPE_F32 && d == kDP) {
+                constexpr int kRowBytes = 128;           // 32 features per pass
+                constexpr int kRegion = 32 * kRowBytes;  // 4 KiB per wave
+                static_assert(L::kKBytes >= kWavesPerGroup * kRegion, "stage regions fit the K buffer");
+                unsigned char* const region = lds_k + wave * kRegion;
+                float* const Of = reinterpret_cast<float*>(Oh);
+                // The lane's position, taken afresh here: the stage addresses
+                // depend on the lane only, and computed before the key loop
+                // they would hold registers through it.
+                int me = lane;
+                asm volatile("" : "+v"(me));
+                const int my_q = me & 31, my_h = me >> 5;
+                const int c = me & 7, sub = me >> 3;  // read side: chunk c of row sub of each 8-row piece
+#pragma unroll
+                for (int pass = 0; pass < 4; ++pass) {
+                    // Features 32 pass .. 32 pass + 31: slots r4 = 2 (pass / 2) + r
+                    // of blocks fb = 2 (pass % 2) + b hold features
+                    // 32 pass + 16 b + 8 r + 4 h (+ 0..3) of row q, i.e. 16-byte
+                    // chunk 4 b + 2 r + h of the pass, stored rotated by the row.
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+#pragma unroll
+                        for (int r = 0; r < 2; ++r) {
+                            const int r4 = 2 * (pass / 2) + r, fb = 2 * (pass % 2) + b;
+                            const float4v value{st.o[fb][4 * r4], st.o[fb][4 * r4 + 1], st.o[fb][4 * r4 + 2],
+                                                st.o[fb][4 * r4 + 3]};
+                            const int chunk = 4 * b + 2 * r + my_h;
+                            *reinterpret_cast<float4v*>(region + my_q * kRowBytes + (((chunk + my_q) & 7) << 4)) =
+                                value * inverse;
+                        }
+                    // Piece i: rows 8 i .. 8 i + 7 of the wave, 8 lanes per row.
+                    // Every read is issued before any store (the reads stay in
+                    // the wave's region; only the stores depend on the row).
+                    float4v piece[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int local = 8 * i + sub;
+                        piece[i] = *reinterpret_cast<const float4v*>(region + local * kRowBytes + (((c + local) & 7) << 4));
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(piece[i]));  // keep the reads here
+                    float* const first = Of + static_cast<std::int64_t>(qw + sub) * p.o_row + 32 * pass + 4 * c;
+                    const std::int64_t piece_step = 8 * p.o_row;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (qw + 8 * i + sub < M)
+                            __builtin_nontemporal_store(piece[i], reinterpret_cast<float4v*>(first + i * piece_step));
+                }
+                return;
+            }
+        }
         if (row < M) {
             const std::int64_t row_offset = static_cast<std::int64_t>(row) * p.o_row;
 #pragma unroll
