@@ -926,22 +926,31 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         const float l = a + b;
         const float inverse = l > 0.0f ? 1.0f / l : 0.0f;
         const int row = qw + q;
-        // fp32 O of 128-feature rows (the variants without dot export) goes
-        // out through LDS. From registers, each store instruction writes 16
+        // fp32 O of 128- and 64-feature rows (the variants without dot export)
+        // goes out through LDS. From registers, each store instruction writes 16
         // bytes to each of 32 rows, i.e. 32 partial cache lines, and those
         // lines, held in the XCD's L2 until written back, evict K / V tiles.
         // Staged, each store writes 8 rows x 128 bytes (full cache lines)
-        // with a non-temporal hint, so O bypasses the L2. The stage buffer is
-        // the K tile buffer: every wave has passed the last tile's second
-        // barrier, so no wave reads it any more and no load targets it. Each
-        // wave stages its 32 rows in four passes of 32 features through a
-        // 4 KiB quarter of it.
-        if constexpr (kVector && !kDots && kDP == 128) {
+        // with a non-temporal hint, so O bypasses the L2. The stage buffers
+        // are the K tile buffer (both 4 KiB regions of it at d = 64, all four
+        // at d = 128) and at d = 64 the V buffer the last tile did not use:
+        // every wave has passed the last tile's second barrier, so no wave
+        // reads them any more and no load targets them. Each wave stages its
+        // 32 rows in kDP / 32 passes of 32 features through a 4 KiB region.
+        if constexpr (kVector && !kDots && (kDP == 128 || kDP == 64)) {
             if (p.o_dtype == TILEMIX_DTYPE_F32 && d == kDP) {
                 constexpr int kRowBytes = 128;           // 32 features per pass
                 constexpr int kRegion = 32 * kRowBytes;  // 4 KiB per wave
-                static_assert(L::kKBytes >= kWavesPerGroup * kRegion, "stage regions fit the K buffer");
-                unsigned char* const region = lds_k + wave * kRegion;
+                constexpr int kPasses = kDP / 32;
+                constexpr int kPassesPerHalf = kPasses / 2;  // passes over features [0, kDP / 2)
+                unsigned char* region;
+                if constexpr (kDP == 128) {
+                    static_assert(L::kKBytes >= kWavesPerGroup * kRegion, "stage regions fit the K buffer");
+                    region = lds_k + wave * kRegion;
+                } else {
+                    static_assert(L::kKBytes >= 2 * kRegion && L::kVBytes >= 2 * kRegion, "stage regions fit K and V");
+                    region = wave < 2 ? lds_k + wave * kRegion : lds_v + (v_buffer ? L::kV1Offset : 0) + (wave - 2) * kRegion;
+                }
                 float* const Of = reinterpret_cast<float*>(Oh);
                 // The lane's position, taken afresh here: the stage addresses
                 // depend on the lane only, and computed before the key loop
@@ -951,16 +960,17 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 const int my_q = me & 31, my_h = me >> 5;
                 const int c = me & 7, sub = me >> 3;  // read side: chunk c of row sub of each 8-row piece
 #pragma unroll
-                for (int pass = 0; pass < 4; ++pass) {
-                    // Features 32 pass .. 32 pass + 31: slots r4 = 2 (pass / 2) + r
-                    // of blocks fb = 2 (pass % 2) + b hold features
+                for (int pass = 0; pass < kPasses; ++pass) {
+                    // Features 32 pass .. 32 pass + 31: slots
+                    // r4 = 2 (pass / kPassesPerHalf) + r of blocks
+                    // fb = 2 (pass % kPassesPerHalf) + b hold features
                     // 32 pass + 16 b + 8 r + 4 h (+ 0..3) of row q, i.e. 16-byte
                     // chunk 4 b + 2 r + h of the pass, stored rotated by the row.
 #pragma unroll
                     for (int b = 0; b < 2; ++b)
 #pragma unroll
                         for (int r = 0; r < 2; ++r) {
-                            const int r4 = 2 * (pass / 2) + r, fb = 2 * (pass % 2) + b;
+                            const int r4 = 2 * (pass / kPassesPerHalf) + r, fb = 2 * (pass % kPassesPerHalf) + b;
                             const float4v value{st.o[fb][4 * r4], st.o[fb][4 * r4 + 1], st.o[fb][4 * r4 + 2],
                                                 st.o[fb][4 * r4 + 3]};
                             const int chunk = 4 * b + 2 * r + my_h;
