@@ -897,12 +897,96 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         }
     }
 
+    // fp32 rows of 128 or 64 features (O, or a split's partial rows) leave
+    // the variants without dot export through LDS. From registers, each
+    // store instruction writes 16 bytes to each of 32 rows, i.e. 32 partial
+    // cache lines, and those lines, held in the XCD's L2 until written back,
+    // evict K / V tiles. Staged, each store writes 8 rows x 128 bytes (full
+    // cache lines) with a non-temporal hint, so the rows bypass the L2. The stage buffers
+    // are the K tile buffer (both 4 KiB regions of it at d = 64, all four
+    // at d = 128) and at d = 64 the V buffer the last tile did not use:
+    // every wave has passed the last tile's second barrier, so no wave
+    // reads them any more and no load targets them. Each wave stages its
+    // 32 rows in kDP / 32 passes of 32 features through a 4 KiB region.
+    // out / out_row: the head's first row and the distance between rows, in
+    // floats; every value is multiplied by factor.
+    constexpr bool kStaged = kVector && !kDots && (kDP == 128 || kDP == 64);
+    auto store_staged = [&](float* out, std::int64_t out_row, float factor) {
+        if constexpr (kStaged) {
+            constexpr int kRowBytes = 128;           // 32 features per pass
+            constexpr int kRegion = 32 * kRowBytes;  // 4 KiB per wave
+            constexpr int kPasses = kDP / 32;
+            constexpr int kPassesPerHalf = kPasses / 2;  // passes over features [0, kDP / 2)
+            unsigned char* region;
+            if constexpr (kDP == 128) {
+                static_assert(L::kKBytes >= kWavesPerGroup * kRegion, "stage regions fit the K buffer");
+                region = lds_k + wave * kRegion;
+            } else {
+                static_assert(L::kKBytes >= 2 * kRegion && L::kVBytes >= 2 * kRegion, "stage regions fit K and V");
+                region = wave < 2 ? lds_k + wave * kRegion : lds_v + (v_buffer ? L::kV1Offset : 0) + (wave - 2) * kRegion;
+            }
+            // The lane's position, taken afresh here: the stage addresses
+            // depend on the lane only, and computed before the key loop
+            // they would hold registers through it.
+            int me = lane;
+            asm volatile("" : "+v"(me));
+            const int my_q = me & 31, my_h = me >> 5;
+            const int c = me & 7, sub = me >> 3;  // read side: chunk c of row sub of each 8-row piece
+    #pragma unroll
+            for (int pass = 0; pass < kPasses; ++pass) {
+                // Features 32 pass .. 32 pass + 31: slots
+                // r4 = 2 (pass / kPassesPerHalf) + r of blocks
+                // fb = 2 (pass % kPassesPerHalf) + b hold features
+                // 32 pass + 16 b + 8 r + 4 h (+ 0..3) of row q, i.e. 16-byte
+                // chunk 4 b + 2 r + h of the pass, stored rotated by the row.
+    #pragma unroll
+                for (int b = 0; b < 2; ++b)
+    #pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        const int r4 = 2 * (pass / kPassesPerHalf) + r, fb = 2 * (pass % kPassesPerHalf) + b;
+                        const float4v value{st.o[fb][4 * r4], st.o[fb][4 * r4 + 1], st.o[fb][4 * r4 + 2],
+                                            st.o[fb][4 * r4 + 3]};
+                        const int chunk = 4 * b + 2 * r + my_h;
+                        *reinterpret_cast<float4v*>(region + my_q * kRowBytes + (((chunk + my_q) & 7) << 4)) =
+                            value * factor;
+                    }
+                // Piece i: rows 8 i .. 8 i + 7 of the wave, 8 lanes per row.
+                // Every read is issued before any store (the reads stay in
+                // the wave's region; only the stores depend on the row).
+                float4v piece[4];
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int local = 8 * i + sub;
+                    piece[i] = *reinterpret_cast<const float4v*>(region + local * kRowBytes + (((c + local) & 7) << 4));
+                }
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(piece[i]));  // keep the reads here
+                float* const first = out + static_cast<std::int64_t>(qw + sub) * out_row + 32 * pass + 4 * c;
+                const std::int64_t piece_step = 8 * out_row;
+    #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (qw + 8 * i + sub < M)
+                        __builtin_nontemporal_store(piece[i], reinterpret_cast<float4v*>(first + i * piece_step));
+            }
+        }
+    };
     // ---------------------------------------------------------- epilogue
     if constexpr (kSplit) {
         // This split's unnormalised rows and their (m, l), for the combine.
         float a = st.lsum, b = st.lsum;
         permlane32_swap(a, b);
         const int row = qw + q;
+        if constexpr (kStaged) {
+            if (d == kDP) {
+                store_staged(p.part_o + static_cast<std::int64_t>(split) * M * d, d, 1.0f);
+                if (row < M && h == 0) {
+                    float* const ml = p.part_ml + 2 * (static_cast<std::int64_t>(split) * M + row);
+                    ml[0] = st.m;
+                    ml[1] = a + b;
+                }
+                return;
+            }
+        }
         if (row < M) {
             unsigned char* const part = reinterpret_cast<unsigned char*>(p.part_o + static_cast<std::int64_t>(split) * M * d);
             const std::int64_t row_offset = static_cast<std::int64_t>(row) * d;
@@ -926,75 +1010,9 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
         const float l = a + b;
         const float inverse = l > 0.0f ? 1.0f / l : 0.0f;
         const int row = qw + q;
-        // fp32 O of 128- and 64-feature rows (the variants without dot export)
-        // goes out through LDS. From registers, each store instruction writes 16
-        // bytes to each of 32 rows, i.e. 32 partial cache lines, and those
-        // lines, held in the XCD's L2 until written back, evict K / V tiles.
-        // Staged, each store writes 8 rows x 128 bytes (full cache lines)
-        // with a non-temporal hint, so O bypasses the L2. The stage buffers
-        // are the K tile buffer (both 4 KiB regions of it at d = 64, all four
-        // at d = 128) and at d = 64 the V buffer the last tile did not use:
-        // every wave has passed the last tile's second barrier, so no wave
-        // reads them any more and no load targets them. Each wave stages its
-        // 32 rows in kDP / 32 passes of 32 features through a 4 KiB region.
-        if constexpr (kVector && !kDots && (kDP == 128 || kDP == 64)) {
+        if constexpr (kStaged) {
             if (p.o_dtype == TILEMIX_DTYPE_F32 && d == kDP) {
-                constexpr int kRowBytes = 128;           // 32 features per pass
-                constexpr int kRegion = 32 * kRowBytes;  // 4 KiB per wave
-                constexpr int kPasses = kDP / 32;
-                constexpr int kPassesPerHalf = kPasses / 2;  // passes over features [0, kDP / 2)
-                unsigned char* region;
-                if constexpr (kDP == 128) {
-                    static_assert(L::kKBytes >= kWavesPerGroup * kRegion, "stage regions fit the K buffer");
-                    region = lds_k + wave * kRegion;
-                } else {
-                    static_assert(L::kKBytes >= 2 * kRegion && L::kVBytes >= 2 * kRegion, "stage regions fit K and V");
-                    region = wave < 2 ? lds_k + wave * kRegion : lds_v + (v_buffer ? L::kV1Offset : 0) + (wave - 2) * kRegion;
-                }
-                float* const Of = reinterpret_cast<float*>(Oh);
-                // The lane's position, taken afresh here: the stage addresses
-                // depend on the lane only, and computed before the key loop
-                // they would hold registers through it.
-                int me = lane;
-                asm volatile("" : "+v"(me));
-                const int my_q = me & 31, my_h = me >> 5;
-                const int c = me & 7, sub = me >> 3;  // read side: chunk c of row sub of each 8-row piece
-#pragma unroll
-                for (int pass = 0; pass < kPasses; ++pass) {
-                    // Features 32 pass .. 32 pass + 31: slots
-                    // r4 = 2 (pass / kPassesPerHalf) + r of blocks
-                    // fb = 2 (pass % kPassesPerHalf) + b hold features
-                    // 32 pass + 16 b + 8 r + 4 h (+ 0..3) of row q, i.e. 16-byte
-                    // chunk 4 b + 2 r + h of the pass, stored rotated by the row.
-#pragma unroll
-                    for (int b = 0; b < 2; ++b)
-#pragma unroll
-                        for (int r = 0; r < 2; ++r) {
-                            const int r4 = 2 * (pass / kPassesPerHalf) + r, fb = 2 * (pass % kPassesPerHalf) + b;
-                            const float4v value{st.o[fb][4 * r4], st.o[fb][4 * r4 + 1], st.o[fb][4 * r4 + 2],
-                                                st.o[fb][4 * r4 + 3]};
-                            const int chunk = 4 * b + 2 * r + my_h;
-                            *reinterpret_cast<float4v*>(region + my_q * kRowBytes + (((chunk + my_q) & 7) << 4)) =
-                                value * inverse;
-                        }
-                    // Piece i: rows 8 i .. 8 i + 7 of the wave, 8 lanes per row.
-                    // Every read is issued before any store (the reads stay in
-                    // the wave's region; only the stores depend on the row).
-                    float4v piece[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int local = 8 * i + sub;
-                        piece[i] = *reinterpret_cast<const float4v*>(region + local * kRowBytes + (((c + local) & 7) << 4));
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(piece[i]));  // keep the reads here
-                    float* const first = Of + static_cast<std::int64_t>(qw + sub) * p.o_row + 32 * pass + 4 * c;
-                    const std::int64_t piece_step = 8 * p.o_row;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (qw + 8 * i + sub < M)
-                            __builtin_nontemporal_store(piece[i], reinterpret_cast<float4v*>(first + i * piece_step));
-                }
+                store_staged(reinterpret_cast<float*>(Oh), p.o_row, inverse);
                 return;
             }
         }
