@@ -932,16 +932,16 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
             asm volatile("" : "+v"(me));
             const int my_q = me & 31, my_h = me >> 5;
             const int c = me & 7, sub = me >> 3;  // read side: chunk c of row sub of each 8-row piece
-    #pragma unroll
+#pragma unroll
             for (int pass = 0; pass < kPasses; ++pass) {
                 // Features 32 pass .. 32 pass + 31: slots
                 // r4 = 2 (pass / kPassesPerHalf) + r of blocks
                 // fb = 2 (pass % kPassesPerHalf) + b hold features
                 // 32 pass + 16 b + 8 r + 4 h (+ 0..3) of row q, i.e. 16-byte
                 // chunk 4 b + 2 r + h of the pass, stored rotated by the row.
-    #pragma unroll
+#pragma unroll
                 for (int b = 0; b < 2; ++b)
-    #pragma unroll
+#pragma unroll
                     for (int r = 0; r < 2; ++r) {
                         const int r4 = 2 * (pass / kPassesPerHalf) + r, fb = 2 * (pass % kPassesPerHalf) + b;
                         const float4v value{st.o[fb][4 * r4], st.o[fb][4 * r4 + 1], st.o[fb][4 * r4 + 2],
@@ -954,16 +954,16 @@ __global__ __launch_bounds__(kThreadsPerGroup, kGroupsPerCU) void attention_kern
                 // Every read is issued before any store (the reads stay in
                 // the wave's region; only the stores depend on the row).
                 float4v piece[4];
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int local = 8 * i + sub;
                     piece[i] = *reinterpret_cast<const float4v*>(region + local * kRowBytes + (((c + local) & 7) << 4));
                 }
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(piece[i]));  // keep the reads here
                 float* const first = out + static_cast<std::int64_t>(qw + sub) * out_row + 32 * pass + 4 * c;
                 const std::int64_t piece_step = 8 * out_row;
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < 4; ++i)
                     if (qw + 8 * i + sub < M)
                         __builtin_nontemporal_store(piece[i], reinterpret_cast<float4v*>(first + i * piece_step));
