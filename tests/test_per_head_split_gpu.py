@@ -8,7 +8,7 @@ library's fixed device workspace).
   device through one event): every head equals the fp64 TileMix oracle.
 * Ragged shapes and both O alignments (vector / element-wise combine) against
   the oracle, with the routing trace and INT32 dots exact; two of them have
-  more splits than the combine takes in one batch (32 and 19).
+  more splits than the combine takes in one batch (64 and 47).
 * A call made while its stream is captured into a graph takes the plain launch
   (no workspace, no event): every replay equals the first, and the oracle.
 """
@@ -99,7 +99,7 @@ def test_split_calls_on_two_streams(tm, oracle_lib, cuda):
 @pytest.mark.parametrize("m,n,d,lead", [(1000, 2500, 128, 4), (1000, 2500, 128, 1), (777, 3001, 48, 4),
                                         (512, 1024, 32, 4), (128, 8192, 128, 4), (300, 6000, 64, 1)],
                          ids=["ragged-vector", "ragged-scalar", "d48", "small",
-                              "32-splits", "19-splits-scalar"])
+                              "64-splits", "47-splits-scalar"])
 def test_split_ragged_shapes(tm, oracle_lib, cuda, m, n, d, lead):
     import torch
 

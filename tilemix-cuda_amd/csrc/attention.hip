@@ -1221,11 +1221,15 @@ static __device__ __align__(256) float split_scratch[kSplitScratchFloats];
 namespace tilemix {
 namespace {
 
-// A split covers at least this many key tiles, so that its prologue (the
-// Q block's load) and its partial-row stores stay small against its loop
-// (measured on 64 per-head calls of 4096 x 4096 x 128: at least 4 tiles per
-// split is level with 2 and faster than 8 or 16).
-constexpr int kMinSplitTiles = 4;
+// A split covers at least this many key tiles, and a head with fewer than
+// kMinSplitHead key tiles is not split: the split's fixed cost (partial rows,
+// the combine launch, the ordering event) is about that of a few tiles'
+// walk. Measured per call (M = 4096, d = 128): at N = 256 the plain launch
+// is 23 % faster than two splits; at N = 512 four 2-tile splits are 14 %
+// faster than two 4-tile ones, and the reference demo (16 tiles) 7 % with 8
+// splits than with 4; from N = 4096 on the slot count limits the splits.
+constexpr int kMinSplitTiles = 2;
+constexpr int kMinSplitHead = 8;
 
 struct SplitDevice {
     float* scratch = nullptr;
@@ -1243,15 +1247,17 @@ SplitDevice* split_devices() {
     return devices;
 }
 
-// Key-range splits for a single-head, non-causal launch that would fill less
-// than half of the device's workgroup slots: as many as bring it to one
-// wave of workgroups, each covering at least kMinSplitTiles key tiles and
-// all fitting in the workspace (1 = no split).
+// Key-range splits for a single-head, non-causal launch of at least
+// kMinSplitHead key tiles that would fill less than half of the device's
+// workgroup slots: as many as bring it to one wave of workgroups, each
+// covering at least kMinSplitTiles key tiles and all fitting in the
+// workspace (1 = no split).
 int choose_splits(const AttnParams& p, int compute_units) {
     if (compute_units <= 0 || p.heads != 1 || p.causal) return 1;
     const int resident = compute_units * kGroupsPerCU;
     if (2 * p.q_blocks > resident) return 1;
     const int tiles = (p.N - 1) / kTileKeys + 1;
+    if (tiles < kMinSplitHead) return 1;
     int splits = std::min(resident / p.q_blocks, tiles / kMinSplitTiles);
     while (splits > 1 && static_cast<std::size_t>(splits) * p.M * (p.d + 2) > kSplitScratchFloats) --splits;
     return splits > 1 ? splits : 1;
