@@ -3,11 +3,17 @@
 //
 // M=1000 queries, N=1003 keys, d=128, routing groups of 2 key tiles with the
 // alternating mask 0xaaaa... (odd groups INT8, even groups FP16).
+//
+// `tilemix_demo --rounds R` also times R more rounds of the two calls
+// (quantize_tilemix_qk + launch_fused_fp16_attention) on the null stream with
+// HIP events, after as many untimed ones, and prints the time per round.
 
 #include "attention_fused.h"
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <stdexcept>
 #include <vector>
 
@@ -41,8 +47,14 @@ private:
 
 }  // namespace
 
-int main() {
+int main(int argc, char** argv) {
     try {
+        int rounds = 0;
+        for (int a = 1; a < argc; ++a) {
+            if (std::strcmp(argv[a], "--rounds") == 0 && a + 1 < argc) rounds = std::atoi(argv[++a]);
+            else throw std::runtime_error(std::string("unknown argument: ") + argv[a]);
+        }
+        if (rounds < 0) throw std::runtime_error("--rounds takes a count >= 0");
         constexpr int M = 1000, N = 1003, d = 128, group = 2;
         const std::size_t q_count = static_cast<std::size_t>(M) * d;
         const std::size_t kv_count = static_cast<std::size_t>(N) * d;
@@ -85,6 +97,31 @@ int main() {
         ensure(hipMemcpy(result.data(), out.get(), q_count * sizeof(float), hipMemcpyDeviceToHost), "download");
         std::printf("TileMix attention: M=%d N=%d d=%d output[0]=%.9g\n", M, N, d, result[0]);
         std::printf("Routing: %d key tiles/group, %zu packed words; bit 0=FP16, bit 1=INT8 MFMA\n", group, words);
+        if (rounds > 0) {
+            auto round = [&]() {
+                ensure(quantize_tilemix_qk(dq.get(), dk.get(), q8.get(), k8.get(), q_scales.get(), k_scales.get(), M,
+                                           N, d),
+                       "quantize_tilemix_qk");
+                ensure(launch_fused_fp16_attention(dq.get(), dk.get(), dv.get(), out.get(), M, N, d,
+                                                   1.0f / std::sqrt(static_cast<float>(d)), nullptr, routing,
+                                                   quantized),
+                       "launch_fused_fp16_attention");
+            };
+            for (int r = 0; r < rounds; ++r) round();  // untimed: the clock rises under sustained work
+            hipEvent_t start = nullptr, stop = nullptr;
+            ensure(hipEventCreate(&start), "hipEventCreate");
+            ensure(hipEventCreate(&stop), "hipEventCreate");
+            ensure(hipEventRecord(start, nullptr), "hipEventRecord");
+            for (int r = 0; r < rounds; ++r) round();
+            ensure(hipEventRecord(stop, nullptr), "hipEventRecord");
+            ensure(hipEventSynchronize(stop), "hipEventSynchronize");
+            float ms = 0.0f;
+            ensure(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+            (void)hipEventDestroy(start);
+            (void)hipEventDestroy(stop);
+            std::printf("Timed: %d rounds of quantize_tilemix_qk + launch_fused_fp16_attention, %.2f us per round\n",
+                        rounds, 1000.0f * ms / static_cast<float>(rounds));
+        }
         return 0;
     } catch (const std::exception& error) {
         std::fprintf(stderr, "ERROR: %s\n", error.what());
