@@ -61,10 +61,10 @@ int tilemix_quantize_qk(const uint16_t* Q, const uint16_t* K, int8_t* Q8, int8_t
  * int32) receives the raw int32 dot of every INT8-routed (q, k).
  * Validation order and codes follow src/tilemix.cu:242-266.
  * A head too small to fill the device (its 128-row blocks under half of the
- * workgroup slots) has its key range split over several workgroups per
- * block, whose partial rows go to a fixed 32 MiB device array inside the
- * library (one per GPU) and are merged into O by a second kernel on
- * `stream`. Split calls on one device are ordered through one event (each
+ * workgroup slots) with at least 8 key tiles of 64 has its key range split
+ * over several workgroups per block, whose partial rows go to a fixed 32 MiB
+ * device array inside the library (one per GPU) and are merged into O by a
+ * second kernel on `stream`. Split calls on one device are ordered through one event (each
  * waits for the previous one's merge, on any stream); a call made while
  * `stream` is being captured into a graph takes the unsplit launch.
  */
